@@ -1,0 +1,293 @@
+"""Benchmark of the quantized-linear hot path on one MI355X.
+
+Metric: int4 dequant-GEMV GB/s (% HBM peak) at Qwen2.5-7B
+shapes; prefill GEMM TFLOP/s.
+
+A "step" is one dequant-matmul call over one batch of synthetic inputs that
+are resident in HBM.  The headline ``value`` is the decode GEMV at the
+Qwen2.5-7B down-proj shape (M=1, K=18944, N=3584, int4
+g128): algorithmic bytes (weights + scales + zeros + x + y, each once) per
+step divided by the time per step.  The other BASELINE configs are measured
+the same way and reported under ``extra``.
+
+Method:
+* weights, scales and zeros rotate through enough independent copies that the
+  working set exceeds the 256 MB Infinity Cache, so HBM is really read;
+* the launches are captured in a HIP graph (host launch overhead excluded),
+  the graph is replayed, and HIP events on the replay stream bracket the
+  timed region, with a device synchronisation on both sides;
+* the CPU baseline is the oracle's restatement (numpy dequantize + fp32 BLAS
+  matmul) timed on this host on the same workload (median of a few runs).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only NAME]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (os.path.join(ROOT, "metal-native_amd"), ROOT):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "int4 dequant-GEMV GB/s (% HBM peak) at Qwen2.5-7B shapes; prefill GEMM TFLOP/s"
+HBM_PEAK_GBS = 8000.0
+FP16_MFMA_PEAK_TFLOPS = 2500.0
+CACHE_BYTES = 256 * 2**20
+ROTATE_TARGET = int(1.3 * CACHE_BYTES)
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+# --------------------------------------------------------------------------
+# workloads
+# --------------------------------------------------------------------------
+
+CONFIGS = {
+    # name: (qtype, M, K, N(weight rows), g, epilogue, bound)
+    "cfg1_qwen05b_gate_m1": ("int4", 1, 896, 4864, 64, None, "hbm"),
+    "cfg2_qwen7b_down_m1": ("int4", 1, 18944, 3584, 128, None, "hbm"),
+    "cfg2_qwen7b_down_m4": ("int4", 4, 18944, 3584, 128, None, "hbm"),
+    "cfg2_qwen7b_down_m8": ("int4", 8, 18944, 3584, 128, None, "hbm"),
+    "cfg3_llama3b_qkv_m512": ("int4", 512, 3072, 5120, 128, None, "mfma"),
+    "cfg4_qwen7b_gateup_int8_swiglu_m1": ("int8", 1, 3584, 2 * 18944, 3584, "swiglu", "hbm"),
+    "cfg4_qwen7b_gateup_int8_swiglu_m16": ("int8", 16, 3584, 2 * 18944, 3584, "swiglu", "hbm"),
+    "cfg4_qwen7b_gateup_int8_swiglu_m64": ("int8", 64, 3584, 2 * 18944, 3584, "swiglu", "hbm"),
+}
+HEADLINE = "cfg2_qwen7b_down_m1"
+
+
+def algo_bytes(qtype, M, K, N, g, epi):
+    """Weights + scales + zeros + x + y, each counted once (int8 per-channel:
+    one fp16 scale per row and no zeros read as bytes of the metric)."""
+    G = (K + g - 1) // g
+    w = N * K // 2 if qtype == "int4" else N * K
+    sz = 2 * N * G * 2 if qtype == "int4" else N * G * 2
+    n_out = N // 2 if epi == "swiglu" else N
+    return w + sz + M * K * 2 + M * n_out * 2
+
+
+def flops(M, K, N):
+    return 2.0 * M * N * K
+
+
+def make_weights(qtype, K, N, g, gen, device):
+    import torch
+
+    G = (K + g - 1) // g
+    if qtype == "int4":
+        wp = torch.randint(0, 256, (N, K // 2), dtype=torch.uint8, device=device, generator=gen)
+        s = (torch.rand((N, G), device=device, generator=gen) * 0.015 + 0.005).half()
+        zp = torch.randint(0, 16, (N, G), device=device, generator=gen).float()
+        z = ((zp - 8.0) * s.float()).half()
+    else:
+        wp = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=device, generator=gen)
+        s = (torch.rand((N, G), device=device, generator=gen) * 0.009 + 0.001).half()
+        z = torch.zeros_like(s)
+    return wp, s, z
+
+
+def measure(name, steps, warmup, device):
+    import torch
+
+    import metal_native as mn
+
+    qtype, M, K, N, g, epi, bound = CONFIGS[name]
+    gen = torch.Generator(device=device)
+    gen.manual_seed(0)
+    per_copy = algo_bytes(qtype, M, K, N, g, epi)
+    copies = max(2, min(256, -(-ROTATE_TARGET // per_copy)))
+    weights = [make_weights(qtype, K, N, g, gen, device) for _ in range(copies)]
+    x = torch.randn((M, K), device=device, generator=gen).half()
+    fn = lambda i: mn.dequant_matmul(x, *weights[i % copies], g, qtype, epilogue=epi)
+
+    # graph of L launches cycling through the copies
+    L = copies * max(1, -(-64 // copies)) if copies < 64 else copies
+    stream = torch.cuda.Stream(device)
+    stream.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(stream):
+        for i in range(copies):
+            fn(i)  # eager warm-up: workspace for this stream, code objects loaded
+    torch.cuda.synchronize(device)
+    path = mn.last_path()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for i in range(L):
+            fn(i)
+    reps = max(1, -(-steps // L))
+    wreps = max(1, -(-warmup // L))
+    cur = torch.cuda.current_stream(device)
+    for _ in range(wreps):
+        graph.replay()
+    torch.cuda.synchronize(device)
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    wall0 = time.perf_counter()
+    t0.record(cur)
+    for _ in range(reps):
+        graph.replay()
+    t1.record(cur)
+    torch.cuda.synchronize(device)
+    wall = time.perf_counter() - wall0
+    ms = t0.elapsed_time(t1)
+    n_steps = reps * L
+    us_per_step = ms * 1000.0 / n_steps
+    gbs = per_copy / (us_per_step * 1e-6) / 1e9
+    res = {
+        "us_per_step": round(us_per_step, 3),
+        "GB/s": round(gbs, 1),
+        "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
+        "algo_bytes_per_step": per_copy,
+        "steps": n_steps,
+        "copies_rotated": copies,
+        "working_set_MB": round(copies * per_copy / 2**20, 1),
+        "kernel_path": path,
+        "wall_s": round(wall, 3),
+        "M": M, "K": K, "N": N, "group_size": g, "quant_type": qtype, "epilogue": epi or "none",
+    }
+    n_out = N // 2 if epi == "swiglu" else N
+    tf = flops(M, K, N) / (us_per_step * 1e-6) / 1e12
+    res["TFLOP/s"] = round(tf, 2)
+    res["pct_fp16_mfma_peak"] = round(100 * tf / FP16_MFMA_PEAK_TFLOPS, 2)
+    res["output_shape"] = [M, n_out]
+    del graph
+    del weights
+    torch.cuda.empty_cache()
+    return res
+
+
+# --------------------------------------------------------------------------
+# CPU baseline: the oracle on this host
+# --------------------------------------------------------------------------
+
+def cpu_baseline(reps: int = 3):
+    import numpy as np
+
+    from oracle import mq_oracle as O
+
+    try:
+        from threadpoolctl import threadpool_info
+
+        blas_threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    except Exception:  # noqa: BLE001
+        blas_threads = os.cpu_count() or 1
+    qtype, M, K, N, g, epi, _ = CONFIGS[HEADLINE]
+    x, wp, s, z = O.make_int4_problem(M, K, N, g, seed=0)
+    times_dq, times_mm = [], []
+    for r in range(reps + 1):
+        t0 = time.perf_counter()
+        w = O.dequant_int4(wp, s, z, K, g)
+        t1 = time.perf_counter()
+        y = O.matmul_f32acc(x, w).astype(np.float16)
+        t2 = time.perf_counter()
+        if r:  # first run is warm-up
+            times_dq.append(t1 - t0)
+            times_mm.append(t2 - t1)
+    dq, mm = float(np.median(times_dq)), float(np.median(times_mm))
+    total = dq + mm
+    by = algo_bytes(qtype, M, K, N, g, epi)
+    del y
+    return {
+        "value": round(by / total / 1e9, 3),
+        "unit": "GB/s",
+        "cores": blas_threads,
+        "kind": "port",
+        "sample": (f"{HEADLINE} full problem (M={M},K={K},N={N},g={g}) on the host: oracle numpy "
+                   f"dequantize (single-threaded) then fp32 BLAS matmul ({blas_threads} threads) and fp16 "
+                   f"round; median of {reps} runs after 1 warm-up; dequant {dq*1e3:.1f} ms + matmul "
+                   f"{mm*1e3:.1f} ms"),
+        "ms_per_step": round(total * 1e3, 2),
+    }
+
+
+# --------------------------------------------------------------------------
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-reps", type=int, default=3)
+    ap.add_argument("--only", default=None, help="comma-separated config names (headline always runs)")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(the kernels shard by weight rows; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        sys.exit(1)
+    import metal_native  # noqa: F401  (fails loudly if the library is not built)
+
+    device = torch.device("cuda:0")
+    names = list(CONFIGS)
+    if args.only:
+        want = set(args.only.split(",")) | {HEADLINE}
+        names = [n for n in names if n in want]
+    results = {}
+    for n in names:
+        log(f"[bench] {n} ...")
+        steps = args.steps if n == HEADLINE else max(200, args.steps // 4)
+        results[n] = measure(n, steps, args.warmup, device)
+        log(f"[bench] {n}: {json.dumps(results[n])}")
+    head = results[HEADLINE]
+
+    cpu = None
+    if not args.no_cpu:
+        log("[bench] cpu baseline ...")
+        cpu = cpu_baseline(args.cpu_reps)
+        log(f"[bench] cpu: {json.dumps(cpu)}")
+
+    achieved = head["GB/s"]
+    line = {
+        "metric": METRIC,
+        "value": achieved,
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": head["steps"],
+        "warmup": args.warmup,
+        "ms_per_step": round(head["us_per_step"] / 1000.0, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic (seeded torch RNG on device; int4 nibbles U{0..15}, scales U(0.005,0.02), "
+                "zero-points U{0..15}, x ~ N(0,1))",
+        "config": {
+            "workload": "BASELINE config 2: Qwen2.5-7B down-proj int4 g128 dequant-GEMV, M=1, K=18944, N=3584",
+            "kernel": "skinny split-K MFMA (v_mfma_f32_16x16x32_f16), fp32 accumulation",
+            "weights_rotated": head["copies_rotated"],
+            "working_set_MB": head["working_set_MB"],
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+        },
+        "cpu_baseline": cpu,
+        "extra": results,
+    }
+    prefill = results.get("cfg3_llama3b_qkv_m512")
+    if prefill:
+        line["prefill_TFLOP/s"] = prefill["TFLOP/s"]
+        line["prefill_frac_fp16_mfma_peak"] = round(prefill["TFLOP/s"] / FP16_MFMA_PEAK_TFLOPS, 4)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

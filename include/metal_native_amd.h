@@ -1,0 +1,122 @@
+/* C ABI of the MI355X (gfx950) quantized-linear library, libmetal_native_amd.so.
+ *
+ * Drop-in for MetalNative's quantized-weight linear path.  Every entry point
+ * takes plain device pointers, sizes and a HIP stream (as void*; NULL = the
+ * null stream), launches asynchronously on that stream and returns a status
+ * code.  The status codes keep the numbering of the reference's
+ * MetalNativeError (include/metal_native/core/error.h:21-31).  On failure a
+ * message is available from mq_last_error() (thread-local), mirroring the
+ * MNException text the reference throws (src/ops/matmul.mm:910-934).
+ *
+ * Storage formats (the reference's, unchanged):
+ *   int4 weights   uint8 [N, K/2]: byte j of row n holds k=2j in the low nibble
+ *                  and k=2j+1 in the high nibble
+ *                  (shaders/matmul_dequant_kernel.metal:37-38,129-139)
+ *   int8 weights   int8 [N, K]
+ *   scales, zeros  fp16 [N, ceil(K/group_size)], row-major
+ *   activations    fp16 [M, K];  output fp16 [M, N] (N/2 columns for SwiGLU)
+ * Dequant: w = half(q-8)*s - z (int4), half(q)*s - z (int8), two fp16 roundings
+ * (shaders/matmul_dequant_kernel.metal:42-43,47-49).
+ */
+#ifndef METAL_NATIVE_AMD_H
+#define METAL_NATIVE_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MQ_API __attribute__((visibility("default")))
+
+/* include/metal_native/core/error.h:21-31 (MetalNativeError) */
+enum mq_status {
+  MQ_SUCCESS = 0,
+  MQ_DEVICE_NOT_FOUND = 1,
+  MQ_ALLOCATION_FAILED = 2,
+  MQ_KERNEL_COMPILATION_FAILED = 3,
+  MQ_INVALID_ARGUMENT = 4,
+  MQ_OUT_OF_MEMORY = 5,
+  MQ_TIMEOUT_ERROR = 6,
+  MQ_INTERNAL_ERROR = 7,
+  MQ_NOT_IMPLEMENTED = 8
+};
+
+/* include/metal_native/ops/matmul.h:60-63 (QuantType) */
+enum mq_quant_type { MQ_QUANT_INT4 = 0, MQ_QUANT_INT8 = 1 };
+
+/* Epilogue applied to the fp32 accumulator before the fp16 store.
+ * BIAS: half(acc + float(bias[n]))  (shaders/matmul_fused_epilogue.metal:108-110)
+ * SWIGLU: weight rows [0,N/2) are gate, [N/2,N) up; output [M, N/2] =
+ *   half(silu(float(half(gate))) * float(half(up))), i.e. the reference's
+ *   dequant_matmul followed by fast::swiglu (shaders/fused_swiglu.metal:48-84)
+ *   in one kernel. */
+enum mq_epilogue { MQ_EPILOGUE_NONE = 0, MQ_EPILOGUE_BIAS = 1, MQ_EPILOGUE_SWIGLU = 2 };
+
+/* Fused dequantize + matmul: out = epi(A . deq(W)^T).
+ * Replaces metal_native::dequant_matmul (include/metal_native/ops/matmul.h:77-82,
+ * src/ops/matmul.mm:903-1029; bound as _C.dequant_matmul at
+ * bindings/bind_ops.cpp:366-382).  Strides are in elements for A/out and in
+ * bytes for the weights (ldw_bytes; K/2 for packed int4 rows, K for int8).
+ * workspace: device memory of at least mq_dequant_matmul_workspace_size()
+ * bytes whose first 256-byte-aligned counter region is zero before the first
+ * call; every call leaves it zero again.  Calls that share a workspace must be
+ * ordered on one stream.  May be NULL when the size query returns 0. */
+MQ_API int mq_dequant_matmul(const void* activations, int64_t lda, const void* weights_packed,
+                             int64_t ldw_bytes, const void* scales, const void* zeros, void* out,
+                             int64_t ldc, int64_t M, int64_t N, int64_t K, int32_t group_size,
+                             int32_t quant_type, int32_t epilogue, const void* bias, void* workspace,
+                             size_t workspace_bytes, void* stream);
+
+/* Workspace bytes mq_dequant_matmul needs for this problem on the current
+ * device (0 when no split-K combine is used). */
+MQ_API size_t mq_dequant_matmul_workspace_size(int64_t M, int64_t N, int64_t K, int32_t group_size,
+                                               int32_t quant_type, int32_t epilogue);
+
+/* Dequantize to fp16 out[N, K] (row stride ldo elements).
+ * flat_groups == 0: per-row groups scales[n, k/g], optional zeros (NULL = no
+ *   zero term) -- the fused kernels' dequant (matmul_dequant_kernel.metal:128-162).
+ * flat_groups != 0: the standalone kernels' semantics, group index i/g over the
+ *   flattened element index and no zero term (shaders/dequantize_kernel.metal:9-163,
+ *   dispatched by QuantWeightCache::get_dequantized,
+ *   src/memory/quant_weight_cache.mm:65-153); zeros must be NULL. */
+MQ_API int mq_dequantize(const void* weights_packed, int64_t ldw_bytes, const void* scales,
+                         const void* zeros, void* out, int64_t ldo, int64_t N, int64_t K,
+                         int32_t group_size, int32_t quant_type, int32_t flat_groups, void* stream);
+
+/* fp16 matmul route for M <= 8: C[M,N] = A[M,K] . op(B), fp32 accumulation.
+ * transpose_b != 0: B is [N, K] (nn.Linear weight, python/metal_native/nn/linear.py:47-49);
+ * transpose_b == 0: B is [K, N].  Replaces matmul_vecmat
+ * (src/ops/matmul.mm:192-298, shaders/matmul_vecmat_kernel.metal:32-456) following
+ * the documented contract C = A @ op(B) (include/metal_native/ops/matmul.h:18-37).
+ * workspace as for mq_dequant_matmul (size from mq_vecmat_f16_workspace_size). */
+MQ_API int mq_vecmat_f16(const void* a, int64_t lda, const void* b, int64_t ldb, void* c, int64_t ldc,
+                         int64_t M, int64_t N, int64_t K, int32_t transpose_b, void* workspace,
+                         size_t workspace_bytes, void* stream);
+MQ_API size_t mq_vecmat_f16_workspace_size(int64_t M, int64_t N, int64_t K, int32_t transpose_b);
+
+/* out[i] = half(silu(float(gate[i])) * float(up[i])), i < n.
+ * Replaces fast::swiglu (src/future/future_stubs.mm:61-101, bound as
+ * _C.fast.swiglu at bindings/bind_ops.cpp:84-93). */
+MQ_API int mq_swiglu_f16(const void* gate, const void* up, void* out, int64_t n, void* stream);
+
+/* Kernel-path override for tests and tuning (no reference counterpart).
+ * key "force_path": 0 = automatic, 1 = skinny split-K MFMA, 2 = tiled MFMA,
+ * 3 = generic.  key "skinny_wg_per_cu": workgroups per CU the split-K planner
+ * aims for (default 4).  Returns MQ_INVALID_ARGUMENT for an unknown key. */
+MQ_API int mq_set_option(const char* key, int64_t value);
+
+/* Kernel the last successful mq_dequant_matmul / mq_vecmat_f16 call on this
+ * thread launched: 1 skinny, 2 tiled, 3 generic, 4 vecmat [K,N]. */
+MQ_API int mq_last_path(void);
+
+MQ_API const char* mq_last_error(void);
+MQ_API const char* mq_error_to_string(int code);
+MQ_API int mq_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* METAL_NATIVE_AMD_H */

@@ -1,0 +1,274 @@
+// C-ABI entry points: argument validation (mirroring src/ops/matmul.mm:910-934),
+// kernel-path selection and launch.  No allocation happens here: outputs and
+// workspace are the caller's.
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/metal_native_amd.h"
+#include "mq_launch.hpp"
+
+namespace {
+
+thread_local std::string g_last_error;
+thread_local int g_last_path = 0;
+std::atomic<int> g_force_path{0};
+std::atomic<int> g_wg_per_cu{4};
+
+int fail(int code, const std::string& msg) {
+  g_last_error = msg;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  g_last_error = std::string(what) + ": " + hipGetErrorString(e);
+  return e == hipErrorOutOfMemory ? MQ_OUT_OF_MEMORY : MQ_INTERNAL_ERROR;
+}
+
+int num_cus_current() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
+
+enum Path { PATH_AUTO = 0, PATH_SKINNY = 1, PATH_TILED = 2, PATH_GENERIC = 3, PATH_VECMAT_KN = 4 };
+
+int choose_path(const mq::LinearArgs& a) {
+  int forced = g_force_path.load();
+  if (forced == PATH_SKINNY && mq::skinny_supported(a)) return PATH_SKINNY;
+  if (forced == PATH_TILED && mq::tiled_supported(a)) return PATH_TILED;
+  if (forced == PATH_GENERIC) return PATH_GENERIC;
+  if (a.M <= 64 && mq::skinny_supported(a)) return PATH_SKINNY;
+  if (mq::tiled_supported(a)) return PATH_TILED;
+  return PATH_GENERIC;
+}
+
+mq::SkinnyPlan plan_for(const mq::LinearArgs& a) {
+  return mq::skinny_plan(a, num_cus_current() * g_wg_per_cu.load() / 4, 0);
+}
+
+int run_linear(const mq::LinearArgs& a, void* ws, size_t ws_bytes, hipStream_t s) {
+  int path = choose_path(a);
+  hipError_t e;
+  if (path == PATH_SKINNY) {
+    mq::SkinnyPlan p = plan_for(a);
+    if (p.ws_bytes > 0 && (ws == nullptr || ws_bytes < p.ws_bytes))
+      return fail(MQ_INVALID_ARGUMENT, "dequant_matmul: workspace too small (need " +
+                                           std::to_string(p.ws_bytes) + " bytes)");
+    if (p.ws_bytes > 0 && ((uintptr_t)ws & 255))
+      return fail(MQ_INVALID_ARGUMENT, "dequant_matmul: workspace must be 256-byte aligned");
+    e = mq::skinny_launch(a, p, ws, s);
+  } else if (path == PATH_TILED) {
+    e = mq::tiled_launch(a, s);
+  } else {
+    e = mq::generic_linear_launch(a, s);
+  }
+  if (e != hipSuccess) return hip_fail(e, "dequant_matmul: kernel launch failed");
+  g_last_path = path;
+  return MQ_SUCCESS;
+}
+
+// Shared validation of mq_dequant_matmul / the workspace query.
+int build_args(mq::LinearArgs& a, int64_t M, int64_t N, int64_t K, int32_t group_size,
+               int32_t quant_type, int32_t epilogue) {
+  if (M < 1 || N < 1 || K < 1)
+    return fail(MQ_INVALID_ARGUMENT, "dequant_matmul: M, N and K must be positive");
+  if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX)
+    return fail(MQ_INVALID_ARGUMENT, "dequant_matmul: dimension too large");
+  if (group_size < 1)
+    return fail(MQ_INVALID_ARGUMENT, "dequant_matmul: group_size must be positive");
+  if (quant_type != MQ_QUANT_INT4 && quant_type != MQ_QUANT_INT8)
+    return fail(MQ_INVALID_ARGUMENT, "dequant_matmul: quant_type must be INT4 or INT8");
+  if (quant_type == MQ_QUANT_INT4 && (K & 1))
+    return fail(MQ_INVALID_ARGUMENT, "dequant_matmul: INT4 weights must be [N, K/2] with K even");
+  if (epilogue < MQ_EPILOGUE_NONE || epilogue > MQ_EPILOGUE_SWIGLU)
+    return fail(MQ_INVALID_ARGUMENT, "dequant_matmul: unknown epilogue");
+  if (epilogue == MQ_EPILOGUE_SWIGLU && (N & 1))
+    return fail(MQ_INVALID_ARGUMENT, "dequant_matmul: SwiGLU needs an even number of weight rows");
+  a.M = (int)M;
+  a.N = (int)N;
+  a.K = (int)K;
+  a.g = group_size;
+  a.G = (int)((K + group_size - 1) / group_size);
+  a.fmt = quant_type == MQ_QUANT_INT4 ? mq::FMT_INT4 : mq::FMT_INT8;
+  a.epi = epilogue;
+  a.F = epilogue == MQ_EPILOGUE_SWIGLU ? (int)(N / 2) : 0;
+  return MQ_SUCCESS;
+}
+
+}  // namespace
+
+extern "C" {
+
+MQ_API int mq_dequant_matmul(const void* activations, int64_t lda, const void* weights_packed,
+                             int64_t ldw_bytes, const void* scales, const void* zeros, void* out,
+                             int64_t ldc, int64_t M, int64_t N, int64_t K, int32_t group_size,
+                             int32_t quant_type, int32_t epilogue, const void* bias, void* workspace,
+                             size_t workspace_bytes, void* stream) {
+  mq::LinearArgs a{};
+  int rc = build_args(a, M, N, K, group_size, quant_type, epilogue);
+  if (rc != MQ_SUCCESS) return rc;
+  if (!activations || !weights_packed || !scales || !out)
+    return fail(MQ_INVALID_ARGUMENT, "dequant_matmul: null pointer argument");
+  if (epilogue == MQ_EPILOGUE_BIAS && !bias)
+    return fail(MQ_INVALID_ARGUMENT, "dequant_matmul: bias epilogue needs a bias pointer");
+  const int64_t row_bytes = quant_type == MQ_QUANT_INT4 ? K / 2 : K;
+  if (lda < K) return fail(MQ_INVALID_ARGUMENT, "dequant_matmul: lda must be >= K");
+  if (ldw_bytes < row_bytes)
+    return fail(MQ_INVALID_ARGUMENT, quant_type == MQ_QUANT_INT4
+                                         ? "dequant_matmul: INT4 weights must be [N, K/2]"
+                                         : "dequant_matmul: INT8 weights must be [N, K]");
+  if (ldc < (epilogue == MQ_EPILOGUE_SWIGLU ? N / 2 : N))
+    return fail(MQ_INVALID_ARGUMENT, "dequant_matmul: ldc too small");
+  a.A = activations; a.lda = lda;
+  a.W = weights_packed; a.ldw = ldw_bytes;
+  a.scales = scales; a.zeros = zeros; a.bias = bias;
+  a.C = out; a.ldc = ldc;
+  return run_linear(a, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+MQ_API size_t mq_dequant_matmul_workspace_size(int64_t M, int64_t N, int64_t K, int32_t group_size,
+                                               int32_t quant_type, int32_t epilogue) {
+  mq::LinearArgs a{};
+  if (build_args(a, M, N, K, group_size, quant_type, epilogue) != MQ_SUCCESS) return 0;
+  // alignment-independent shape checks only: assume aligned operands
+  a.lda = K; a.ldw = quant_type == MQ_QUANT_INT4 ? K / 2 : K; a.ldc = N;
+  a.A = (const void*)256; a.W = (const void*)256;
+  if (a.ldw & 15) return 0;
+  if (choose_path(a) != PATH_SKINNY) return 0;
+  return plan_for(a).ws_bytes;
+}
+
+MQ_API int mq_dequantize(const void* weights_packed, int64_t ldw_bytes, const void* scales,
+                         const void* zeros, void* out, int64_t ldo, int64_t N, int64_t K,
+                         int32_t group_size, int32_t quant_type, int32_t flat_groups, void* stream) {
+  if (!weights_packed || !scales || !out) return fail(MQ_INVALID_ARGUMENT, "dequantize: null pointer argument");
+  if (N < 1 || K < 1 || N * K > ((int64_t)1 << 40)) return fail(MQ_INVALID_ARGUMENT, "dequantize: bad shape");
+  if (group_size < 1) return fail(MQ_INVALID_ARGUMENT, "dequantize: group_size must be positive");
+  if (quant_type != MQ_QUANT_INT4 && quant_type != MQ_QUANT_INT8)
+    return fail(MQ_INVALID_ARGUMENT, "dequantize: quant_type must be INT4 or INT8");
+  if (flat_groups && zeros) return fail(MQ_INVALID_ARGUMENT, "dequantize: flat groups take no zeros");
+  if (!flat_groups && quant_type == MQ_QUANT_INT4 && (K & 1))
+    return fail(MQ_INVALID_ARGUMENT, "dequantize: INT4 rows need an even K");
+  if (ldo < K) return fail(MQ_INVALID_ARGUMENT, "dequantize: ldo must be >= K");
+  if (!flat_groups && ldw_bytes < (quant_type == MQ_QUANT_INT4 ? K / 2 : K))
+    return fail(MQ_INVALID_ARGUMENT, "dequantize: weight rows too short");
+  mq::DequantArgs a{};
+  a.W = weights_packed; a.ldw = ldw_bytes;
+  a.scales = scales; a.zeros = zeros;
+  a.out = out; a.ldo = ldo;
+  a.N = (int)N; a.K = (int)K; a.g = group_size;
+  a.G = (int)((K + group_size - 1) / group_size);
+  a.fmt = quant_type == MQ_QUANT_INT4 ? mq::FMT_INT4 : mq::FMT_INT8;
+  a.flat = flat_groups ? 1 : 0;
+  if (a.flat) {  // flat layout is one contiguous element range
+    a.ldw = quant_type == MQ_QUANT_INT4 ? K / 2 : K;
+    if (a.ldo != K) return fail(MQ_INVALID_ARGUMENT, "dequantize: flat groups need ldo == K");
+  }
+  hipError_t e = mq::dequantize_launch(a, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "dequantize: kernel launch failed");
+  return MQ_SUCCESS;
+}
+
+MQ_API int mq_vecmat_f16(const void* a, int64_t lda, const void* b, int64_t ldb, void* c, int64_t ldc,
+                         int64_t M, int64_t N, int64_t K, int32_t transpose_b, void* workspace,
+                         size_t workspace_bytes, void* stream) {
+  if (!a || !b || !c) return fail(MQ_INVALID_ARGUMENT, "matmul: null pointer argument");
+  if (M < 1 || N < 1 || K < 1 || M > INT32_MAX || N > INT32_MAX || K > INT32_MAX)
+    return fail(MQ_INVALID_ARGUMENT, "matmul: bad shape");
+  if (lda < K || ldc < N || ldb < (transpose_b ? K : N))
+    return fail(MQ_INVALID_ARGUMENT, "matmul: leading dimension too small");
+  if (!transpose_b) {
+    hipError_t e = mq::vecmat_kn_launch(a, lda, b, ldb, c, ldc, (int)M, (int)N, (int)K, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "matmul: kernel launch failed");
+    g_last_path = PATH_VECMAT_KN;
+    return MQ_SUCCESS;
+  }
+  mq::LinearArgs la{};
+  la.A = a; la.lda = lda;
+  la.W = b; la.ldw = ldb * 2;
+  la.C = c; la.ldc = ldc;
+  la.M = (int)M; la.N = (int)N; la.K = (int)K;
+  la.g = 1; la.G = 1;
+  la.fmt = mq::FMT_F16;
+  la.epi = mq::EPI_NONE;
+  int path = choose_path(la);
+  if (path == PATH_TILED) path = PATH_GENERIC;  // the tiled kernel takes quantized weights only
+  if (path == PATH_SKINNY) return run_linear(la, workspace, workspace_bytes, (hipStream_t)stream);
+  hipError_t e = mq::generic_linear_launch(la, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "matmul: kernel launch failed");
+  g_last_path = PATH_GENERIC;
+  return MQ_SUCCESS;
+}
+
+MQ_API size_t mq_vecmat_f16_workspace_size(int64_t M, int64_t N, int64_t K, int32_t transpose_b) {
+  if (!transpose_b || M < 1 || N < 1 || K < 1) return 0;
+  mq::LinearArgs la{};
+  la.A = (const void*)256; la.lda = K;
+  la.W = (const void*)256; la.ldw = K * 2;
+  la.ldc = N;
+  la.M = (int)M; la.N = (int)N; la.K = (int)K;
+  la.g = 1; la.G = 1;
+  la.fmt = mq::FMT_F16;
+  la.epi = mq::EPI_NONE;
+  if (la.ldw & 15) return 0;
+  if (choose_path(la) != PATH_SKINNY) return 0;
+  return plan_for(la).ws_bytes;
+}
+
+MQ_API int mq_swiglu_f16(const void* gate, const void* up, void* out, int64_t n, void* stream) {
+  if (!gate || !up || !out) return fail(MQ_INVALID_ARGUMENT, "fast::swiglu: null pointer argument");
+  if (n < 0) return fail(MQ_INVALID_ARGUMENT, "fast::swiglu: negative size");
+  if (n == 0) return MQ_SUCCESS;
+  hipError_t e = mq::swiglu_launch(gate, up, out, n, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "fast::swiglu: kernel launch failed");
+  return MQ_SUCCESS;
+}
+
+MQ_API int mq_set_option(const char* key, int64_t value) {
+  if (!key) return fail(MQ_INVALID_ARGUMENT, "set_option: null key");
+  if (std::strcmp(key, "force_path") == 0) {
+    if (value < 0 || value > 3) return fail(MQ_INVALID_ARGUMENT, "set_option: force_path must be 0..3");
+    g_force_path.store((int)value);
+    return MQ_SUCCESS;
+  }
+  if (std::strcmp(key, "skinny_wg_per_cu") == 0) {
+    if (value < 1 || value > 64) return fail(MQ_INVALID_ARGUMENT, "set_option: skinny_wg_per_cu must be 1..64");
+    g_wg_per_cu.store((int)value);
+    return MQ_SUCCESS;
+  }
+  return fail(MQ_INVALID_ARGUMENT, std::string("set_option: unknown key ") + key);
+}
+
+MQ_API int mq_last_path(void) { return g_last_path; }
+
+MQ_API const char* mq_last_error(void) { return g_last_error.c_str(); }
+
+MQ_API const char* mq_error_to_string(int code) {
+  switch (code) {
+    case MQ_SUCCESS: return "Success";
+    case MQ_DEVICE_NOT_FOUND: return "DeviceNotFound";
+    case MQ_ALLOCATION_FAILED: return "AllocationFailed";
+    case MQ_KERNEL_COMPILATION_FAILED: return "KernelCompilationFailed";
+    case MQ_INVALID_ARGUMENT: return "InvalidArgument";
+    case MQ_OUT_OF_MEMORY: return "OutOfMemory";
+    case MQ_TIMEOUT_ERROR: return "TimeoutError";
+    case MQ_INTERNAL_ERROR: return "InternalError";
+    case MQ_NOT_IMPLEMENTED: return "NotImplemented";
+    default: return "Unknown";
+  }
+}
+
+MQ_API int mq_abi_version(void) { return 1; }
+
+}  // extern "C"

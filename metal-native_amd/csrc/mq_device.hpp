@@ -1,0 +1,128 @@
+// Device-side building blocks for the quantized-linear kernels (gfx950 only).
+//
+// Storage formats are the reference's (kimsejun0629/metal-native):
+//   int4: uint8 [N, K/2], byte j of row n = (k=2j low nibble, k=2j+1 high
+//         nibble)  -- shaders/matmul_dequant_kernel.metal:37-38,129-139
+//   int8: int8  [N, K]                    -- matmul_dequant_kernel.metal:400-412
+//   scales/zeros: fp16 [N, ceil(K/g)], group of k is k/g  -- :98,141-143
+// Dequant: w = half(q-8)*s - z (int4), w = half(q)*s - z (int8), two fp16
+// roundings, multiply first (matmul_dequant_kernel.metal:42-43,47-49).
+//
+// Every translation unit that includes this header disables floating-point
+// contraction so that the multiply and the subtract of the dequant formula are
+// never fused into one FMA (which would round once instead of twice).
+#pragma once
+#pragma clang fp contract(off)
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "mq_launch.hpp"
+
+namespace mq {
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+
+
+// k values covered by one 16-byte load of a weight row.
+template <int FMT> struct FmtTraits;
+template <> struct FmtTraits<FMT_INT4> { static constexpr int KPL = 32; };
+template <> struct FmtTraits<FMT_INT8> { static constexpr int KPL = 16; };
+template <> struct FmtTraits<FMT_F16>  { static constexpr int KPL = 8; };
+
+__device__ __forceinline__ h2 as_h2(uint32_t v) { return __builtin_bit_cast(h2, v); }
+__device__ __forceinline__ uint32_t as_u32(h2 v) { return __builtin_bit_cast(uint32_t, v); }
+
+// Exact fp16 "q - 8" for two nibbles placed at bits [3:0] and [19:16]:
+// 0x6400 is 1024.0, so OR-ing a nibble into the low mantissa bits gives 1024+q
+// exactly, and subtracting 1032 gives q-8 exactly.
+__device__ __forceinline__ h2 nib_lo_pair(uint32_t d) {
+  return as_h2((d & 0x000F000Fu) | 0x64006400u) - (h2){(_Float16)1032.0f, (_Float16)1032.0f};
+}
+// Same for nibbles at bits [7:4] and [23:20]: the halves hold 1024+16q, and
+// (1024+16q)/16 - 72 = q-8.  Every intermediate is exact, so a fused
+// multiply-add is used deliberately here.
+__device__ __forceinline__ h2 nib_hi_pair(uint32_t d) {
+  h2 v = as_h2((d & 0x00F000F0u) | 0x64006400u);
+  return __builtin_elementwise_fma(v, (h2){(_Float16)0.0625f, (_Float16)0.0625f},
+                                   (h2){(_Float16)-72.0f, (_Float16)-72.0f});
+}
+
+// w = RNE(RNE(q*s) - z): one packed multiply and one packed subtract.
+__device__ __forceinline__ h2 scale_sub(h2 q, h2 s, h2 z) {
+  h2 t = q * s;
+  return t - z;
+}
+
+// Eight int4 weights of one dword (k0..k7 at bits 4i) dequantized into the
+// MFMA-operand order [k0,k4,k1,k5,k2,k6,k3,k7].  Activations multiplied
+// against these are staged in the same order (see perm8_int4).
+__device__ __forceinline__ h8 dq_int4_dword_perm(uint32_t d, h2 s, h2 z) {
+  uint32_t d8 = d >> 8;
+  h2 p0 = scale_sub(nib_lo_pair(d), s, z);   // k0, k4
+  h2 p1 = scale_sub(nib_hi_pair(d), s, z);   // k1, k5
+  h2 p2 = scale_sub(nib_lo_pair(d8), s, z);  // k2, k6
+  h2 p3 = scale_sub(nib_hi_pair(d8), s, z);  // k3, k7
+  h8 r;
+  r.s01 = p0; r.s23 = p1; r.s45 = p2; r.s67 = p3;
+  return r;
+}
+
+// Eight int4 weights in natural k order (used where the output is stored,
+// i.e. the dequantize op).  v_perm_b32 copies byte b into bytes 0 and 2 so
+// the two nibbles of one byte land in the two fp16 halves.
+__device__ __forceinline__ h2 nib_byte_pair(uint32_t d, uint32_t sel) {
+  uint32_t e = __builtin_amdgcn_perm(0u, d, sel);  // bytes [b, 0, b, 0]
+  h2 v = as_h2((e & 0x00F0000Fu) | 0x64006400u);   // (1024+lo, 1024+16*hi)
+  return __builtin_elementwise_fma(v, (h2){(_Float16)1.0f, (_Float16)0.0625f},
+                                   (h2){(_Float16)-1032.0f, (_Float16)-72.0f});
+}
+__device__ __forceinline__ h8 dq_int4_dword_nat(uint32_t d, h2 s, h2 z) {
+  h8 r;
+  r.s01 = scale_sub(nib_byte_pair(d, 0x0c000c00u), s, z);
+  r.s23 = scale_sub(nib_byte_pair(d, 0x0c010c01u), s, z);
+  r.s45 = scale_sub(nib_byte_pair(d, 0x0c020c02u), s, z);
+  r.s67 = scale_sub(nib_byte_pair(d, 0x0c030c03u), s, z);
+  return r;
+}
+
+// Four int8 weights of one dword in natural order.  XOR 0x80 turns the signed
+// byte q into q+128 (0..255); v_perm_b32 places it under a 0x64 high byte,
+// giving fp16 1024+q+128 exactly; subtracting 1152 gives q exactly.
+__device__ __forceinline__ void dq_int8_dword(uint32_t d, h2 s, h2 z, h2& lo, h2& hi) {
+  uint32_t u = d ^ 0x80808080u;
+  const h2 off = (h2){(_Float16)1152.0f, (_Float16)1152.0f};
+  h2 q01 = as_h2(__builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) - off;
+  h2 q23 = as_h2(__builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) - off;
+  lo = scale_sub(q01, s, z);
+  hi = scale_sub(q23, s, z);
+}
+
+// Reorder eight fp16 activations (natural k order, as four dwords) into the
+// int4 operand order [x0,x4,x1,x5,x2,x6,x3,x7].
+__device__ __forceinline__ u4 perm8_int4(u4 v) {
+  u4 r;
+  r.x = __builtin_amdgcn_perm(v.z, v.x, 0x05040100u);  // x0 | x4<<16
+  r.y = __builtin_amdgcn_perm(v.z, v.x, 0x07060302u);  // x1 | x5<<16
+  r.z = __builtin_amdgcn_perm(v.w, v.y, 0x05040100u);  // x2 | x6<<16
+  r.w = __builtin_amdgcn_perm(v.w, v.y, 0x07060302u);  // x3 | x7<<16
+  return r;
+}
+
+__device__ __forceinline__ f4 mfma16x16x32(h8 a, h8 b, f4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float silu_f32(float v) { return v / (1.0f + expf(-v)); }
+
+// Scalar dequant of one element (generic kernels).
+__device__ __forceinline__ _Float16 dq_scalar(int q, _Float16 s, _Float16 z) {
+  _Float16 qh = (_Float16)q;
+  _Float16 t = qh * s;
+  return t - z;
+}
+
+}  // namespace mq

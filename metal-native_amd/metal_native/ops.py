@@ -1,0 +1,410 @@
+"""Python-facing ops of the quantized-linear path on PyTorch-ROCm tensors.
+
+Names, argument order, ``quant_type`` string handling and error texts follow
+the reference's pybind11 surface:
+  * ``dequant_matmul``  -- bindings/bind_ops.cpp:366-382 -> src/ops/matmul.mm:903-1029
+  * ``matmul``          -- bindings/bind_ops.cpp:170-183 -> src/ops/matmul.mm:599-882
+                           (the M<=8 vecmat route, select_kernel :167-190)
+  * ``fast.swiglu``     -- bindings/bind_ops.cpp:84-93 -> src/future/future_stubs.mm:61-101
+  * ``MetalNativeError``-- bindings/bind_core.cpp:347 (MNException translation)
+Extensions (no reference counterpart): ``dequantize`` (the dequantize kernels
+are only reachable through QuantWeightCache in the reference,
+src/memory/quant_weight_cache.mm:65-153), ``quantize``, and the ``epilogue`` /
+``bias`` keywords of ``dequant_matmul``.
+
+Every op launches a HIP kernel of libmetal_native_amd.so on the current torch
+stream and returns without synchronising, like the reference's lazy command
+buffers.  Outputs are fresh tensors owned by the caller.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+
+import torch
+
+from . import _lib
+
+_L = _lib.lib
+
+
+class MetalNativeError(RuntimeError):
+    """Mirror of ``_C.MetalNativeError`` (bindings/bind_core.cpp:347).
+
+    ``code`` carries the MetalNativeError number
+    (include/metal_native/core/error.h:21-31)."""
+
+    def __init__(self, message: str, code: int = _lib.INVALID_ARGUMENT):
+        super().__init__(message)
+        self.code = code
+
+
+def _check(rc: int) -> None:
+    if rc != _lib.SUCCESS:
+        msg = _L.mq_last_error().decode()
+        name = _L.mq_error_to_string(rc).decode()
+        raise MetalNativeError(f"{msg} [{name}]", rc)
+
+
+def _invalid(msg: str):
+    raise MetalNativeError(msg, _lib.INVALID_ARGUMENT)
+
+
+def _stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _ptr(t: torch.Tensor | None):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+# ---------------------------------------------------------------------------
+# split-K workspace: one zero-initialised buffer per (device, stream), grown on
+# demand.  The kernels leave its counter region zero after every call, so a
+# buffer is reusable by every later call ordered on the same stream.
+# ---------------------------------------------------------------------------
+_ws_lock = threading.Lock()
+_ws_cache: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def _workspace(device: torch.device, nbytes: int) -> tuple[torch.Tensor | None, int]:
+    if nbytes == 0:
+        return None, 0
+    key = (device.index, _stream_handle(device))
+    with _ws_lock:
+        buf = _ws_cache.get(key)
+        if buf is None or buf.numel() < nbytes:
+            if torch.cuda.is_current_stream_capturing():
+                _invalid("dequant_matmul: split-K workspace must be allocated before graph capture "
+                         "(run the op once eagerly on this stream first)")
+            # round up so that nearby shapes share one buffer
+            size = max(nbytes, 1 << 20)
+            size = 1 << (size - 1).bit_length()
+            buf = torch.zeros(size, dtype=torch.uint8, device=device)
+            _ws_cache[key] = buf
+    return buf, buf.numel()
+
+
+def _require_cuda(t: torch.Tensor, what: str, op: str):
+    if not isinstance(t, torch.Tensor):
+        _invalid(f"{op}: {what} must be a torch.Tensor")
+    if t.device.type != "cuda":
+        _invalid(f"{op}: {what} must be a GPU tensor (got {t.device})")
+
+
+def _rows(t: torch.Tensor, what: str, op: str) -> int:
+    """Row stride (elements) of a 2-D tensor whose last dim is contiguous."""
+    if t.dim() != 2:
+        _invalid(f"{op}: {what} must be 2D")
+    if t.size(1) > 1 and t.stride(1) != 1:
+        _invalid(f"{op}: {what} must be contiguous along its last dimension")
+    return max(t.stride(0), t.size(1)) if t.size(0) > 1 else t.size(1)
+
+
+# ---------------------------------------------------------------------------
+# dequant_matmul
+# ---------------------------------------------------------------------------
+
+_EPILOGUES = {None: _lib.EPILOGUE_NONE, "none": _lib.EPILOGUE_NONE,
+              "bias": _lib.EPILOGUE_BIAS, "swiglu": _lib.EPILOGUE_SWIGLU}
+
+
+def quant_type_code(quant_type: str) -> int:
+    """``"int4"`` selects INT4; any other string selects INT8, as in
+    bindings/bind_ops.cpp:373."""
+    return _lib.QUANT_INT4 if quant_type == "int4" else _lib.QUANT_INT8
+
+
+def dequant_matmul(activations: torch.Tensor, weights_packed: torch.Tensor, scales: torch.Tensor,
+                   zeros: torch.Tensor, group_size: int, quant_type: str, *,
+                   epilogue: str | None = None, bias: torch.Tensor | None = None) -> torch.Tensor:
+    """Fused dequantize + matmul: ``activations[M,K] . deq(weights)[N,K]^T`` -> fp16 ``[M,N]``.
+
+    Validation and messages follow src/ops/matmul.mm:910-934.  Beyond the
+    reference, the dtype/shape/device of weights, scales and zeros are checked
+    too (the reference reads out of bounds on a mismatch), and
+    ``group_size == K`` (one group per row: per-output-channel scales) is
+    accepted as an extension.
+    ``epilogue="bias"`` adds ``bias[N]`` in fp32; ``epilogue="swiglu"`` treats
+    weight rows ``[0,N/2)`` as gate and ``[N/2,N)`` as up and returns
+    ``[M, N/2] = fast.swiglu(gate, up)`` of the fp16 projection.
+    """
+    op = "dequant_matmul"
+    _require_cuda(activations, "activations", op)
+    if activations.dim() != 2:
+        _invalid("dequant_matmul: activations must be 2D [M, K]")
+    if activations.dtype != torch.float16:
+        _invalid("dequant_matmul: activations must be Float16")
+    M, K = activations.shape
+    if group_size not in (32, 64, 128) and group_size != K:
+        _invalid("dequant_matmul: group_size must be 32, 64, or 128")
+    qt = quant_type_code(quant_type)
+    for t, what in ((weights_packed, "weights_packed"), (scales, "scales"), (zeros, "zeros")):
+        _require_cuda(t, what, op)
+        if t.device != activations.device:
+            _invalid(f"{op}: {what} must be on the activations' device")
+    if weights_packed.dim() != 2:
+        _invalid(f"{op}: weights_packed must be 2D")
+    N = weights_packed.shape[0]
+    if qt == _lib.QUANT_INT4:
+        if weights_packed.shape[1] != K // 2:
+            _invalid("dequant_matmul: INT4 weights must be [N, K/2]")
+        if K % 2:
+            _invalid("dequant_matmul: INT4 weights must be [N, K/2] with K even")
+        if weights_packed.dtype not in (torch.uint8, torch.int8):
+            _invalid(f"{op}: INT4 weights must be uint8 (two nibbles per byte)")
+    else:
+        if weights_packed.shape[1] != K:
+            _invalid("dequant_matmul: INT8 weights must be [N, K]")
+        if weights_packed.dtype not in (torch.int8, torch.uint8):
+            _invalid(f"{op}: INT8 weights must be int8")
+    G = (K + group_size - 1) // group_size
+    for t, what in ((scales, "scales"), (zeros, "zeros")):
+        if t.dtype != torch.float16:
+            _invalid(f"{op}: {what} must be Float16")
+        if tuple(t.shape) != (N, G):
+            _invalid(f"{op}: {what} must be [N, ceil(K/group_size)] = [{N}, {G}], got {list(t.shape)}")
+    if epilogue not in _EPILOGUES:
+        _invalid(f"{op}: unknown epilogue {epilogue!r}")
+    epi = _EPILOGUES[epilogue]
+    if epi == _lib.EPILOGUE_BIAS:
+        if bias is None:
+            _invalid(f"{op}: epilogue='bias' needs bias")
+        _require_cuda(bias, "bias", op)
+        if bias.dtype != torch.float16 or bias.numel() != N:
+            _invalid(f"{op}: bias must be Float16 [N]")
+        bias = bias.contiguous()
+    elif bias is not None:
+        _invalid(f"{op}: bias given without epilogue='bias'")
+    if epi == _lib.EPILOGUE_SWIGLU and N % 2:
+        _invalid(f"{op}: SwiGLU needs an even number of weight rows")
+    n_out = N // 2 if epi == _lib.EPILOGUE_SWIGLU else N
+
+    lda = _rows(activations, "activations", op)
+    ldw = _rows(weights_packed, "weights_packed", op)
+    scales = scales.contiguous()
+    zeros = zeros.contiguous()
+    dev = activations.device
+    out = torch.empty((M, n_out), dtype=torch.float16, device=dev)
+    if M == 0 or n_out == 0:
+        return out
+    with torch.cuda.device(dev):
+        need = _L.mq_dequant_matmul_workspace_size(M, N, K, group_size, qt, epi)
+        ws, ws_bytes = _workspace(dev, need)
+        rc = _L.mq_dequant_matmul(
+            _ptr(activations), lda, _ptr(weights_packed), ldw, _ptr(scales), _ptr(zeros), _ptr(out),
+            n_out, M, N, K, group_size, qt, epi, _ptr(bias), _ptr(ws), ws_bytes, _stream_handle(dev))
+    _check(rc)
+    return out
+
+
+# ---------------------------------------------------------------------------
+# dequantize (extension)
+# ---------------------------------------------------------------------------
+
+def dequantize(weights_packed: torch.Tensor, scales: torch.Tensor, zeros: torch.Tensor | None,
+               group_size: int, quant_type: str, *, K: int | None = None,
+               flat_groups: bool = False) -> torch.Tensor:
+    """fp16 ``[N, K]`` weights.
+
+    ``flat_groups=False``: the fused kernels' dequant, ``half(q-8)*s[n,k/g] - z[n,k/g]``
+    (shaders/matmul_dequant_kernel.metal:29-49,128-162); ``zeros=None`` drops
+    the zero term.
+    ``flat_groups=True``: the standalone kernels' semantics,
+    ``out.flat[i] = half(q_i - 8) * scales.flat[i // g]`` with no zero
+    (shaders/dequantize_kernel.metal:9-163 as dispatched by
+    src/memory/quant_weight_cache.mm:96-140); the output has the INT4 packed
+    shape with its last dimension doubled, as there (:81-90).
+    """
+    op = "dequantize"
+    _require_cuda(weights_packed, "weights_packed", op)
+    qt = quant_type_code(quant_type)
+    if weights_packed.dim() != 2:
+        _invalid(f"{op}: weights_packed must be 2D")
+    N, cols = weights_packed.shape
+    if K is None:
+        K = cols * 2 if qt == _lib.QUANT_INT4 else cols
+    if qt == _lib.QUANT_INT4 and cols != K // 2:
+        _invalid("dequantize: INT4 weights must be [N, K/2]")
+    if qt == _lib.QUANT_INT8 and cols != K:
+        _invalid("dequantize: INT8 weights must be [N, K]")
+    if group_size < 1:
+        _invalid(f"{op}: group_size must be positive")
+    _require_cuda(scales, "scales", op)
+    if scales.dtype != torch.float16:
+        _invalid(f"{op}: scales must be Float16")
+    if flat_groups:
+        if zeros is not None:
+            _invalid(f"{op}: flat groups take no zeros")
+        weights_packed = weights_packed.contiguous()
+        need = (N * K + group_size - 1) // group_size
+        if scales.numel() < need:
+            _invalid(f"{op}: scales must hold ceil(N*K/group_size) = {need} values")
+    else:
+        G = (K + group_size - 1) // group_size
+        if tuple(scales.shape) != (N, G):
+            _invalid(f"{op}: scales must be [N, ceil(K/group_size)] = [{N}, {G}]")
+        if zeros is not None:
+            _require_cuda(zeros, "zeros", op)
+            if zeros.dtype != torch.float16 or tuple(zeros.shape) != (N, G):
+                _invalid(f"{op}: zeros must be Float16 [N, ceil(K/group_size)]")
+            zeros = zeros.contiguous()
+    scales = scales.contiguous()
+    ldw = _rows(weights_packed, "weights_packed", op)
+    dev = weights_packed.device
+    out = torch.empty((N, K), dtype=torch.float16, device=dev)
+    if N == 0 or K == 0:
+        return out
+    with torch.cuda.device(dev):
+        rc = _L.mq_dequantize(_ptr(weights_packed), ldw, _ptr(scales), _ptr(zeros), _ptr(out), K, N, K,
+                              group_size, qt, 1 if flat_groups else 0, _stream_handle(dev))
+    _check(rc)
+    return out
+
+
+# ---------------------------------------------------------------------------
+# quantize (extension; the reference has no quantizer)
+# ---------------------------------------------------------------------------
+
+def quantize(w: torch.Tensor, group_size: int, quant_type: str):
+    """Quantize fp16 ``W [N, K]`` into ``(weights_packed, scales, zeros)`` of the
+    reference's storage format; the exact inverse of the dequant formula on
+    weights that lie on the quantization grid.
+
+    int4 (asymmetric, per group): ``s = (max-min)/15``,
+    ``zp = clamp(round(-min/s), 0, 15)``, ``q = clamp(round(w/s)+zp, 0, 15)``,
+    ``zeros = half((zp-8)*s)``, so ``(q-8)*s - zeros ~= (q-zp)*s``.
+    int8 (symmetric, per group): ``s = max|w|/127``, ``q = clamp(round(w/s), -127, 127)``,
+    ``zeros = 0``.
+    Runs as torch ops on ``w``'s device (an offline weight-preparation step).
+    """
+    if w.dim() != 2:
+        _invalid("quantize: weights must be 2D [N, K]")
+    N, K = w.shape
+    qt = quant_type_code(quant_type)
+    if qt == _lib.QUANT_INT4 and K % 2:
+        _invalid("quantize: INT4 needs an even K")
+    g = group_size
+    G = (K + g - 1) // g
+    wf = w.to(torch.float16).to(torch.float32)
+    pad = G * g - K
+    if pad:
+        wf = torch.cat([wf, wf[:, -1:].expand(N, pad)], dim=1)
+    wp = wf.reshape(N, G, g)
+    if qt == _lib.QUANT_INT4:
+        lo = wp.amin(dim=2)
+        hi = wp.amax(dim=2)
+        s = ((hi - lo) / 15.0).to(torch.float16)
+        s = torch.where(s == 0, torch.ones_like(s), s)
+        sf = s.to(torch.float32)
+        zp = torch.clamp(torch.round(-lo / sf), 0, 15)
+        q = torch.clamp(torch.round(wp / sf[:, :, None]) + zp[:, :, None], 0, 15).to(torch.uint8)
+        q = q.reshape(N, G * g)[:, :K]
+        packed = (q[:, 0::2] | (q[:, 1::2] << 4)).contiguous()
+        zeros = ((zp - 8.0) * sf).to(torch.float16)
+        return packed, s, zeros
+    amax = wp.abs().amax(dim=2)
+    s = (amax / 127.0).to(torch.float16)
+    s = torch.where(s == 0, torch.ones_like(s), s)
+    q = torch.clamp(torch.round(wp / s.to(torch.float32)[:, :, None]), -127, 127).to(torch.int8)
+    return q.reshape(N, G * g)[:, :K].contiguous(), s, torch.zeros_like(s)
+
+
+# ---------------------------------------------------------------------------
+# matmul (the fp16 vecmat route) and fast.swiglu
+# ---------------------------------------------------------------------------
+
+def _vecmat_route(M: int, N: int, K: int, dtype: torch.dtype) -> bool:
+    """select_kernel's VecMat condition (src/ops/matmul.mm:177-178), for the
+    dtypes this build has a kernel for."""
+    return M <= 8 and N >= 256 and K >= 256 and dtype == torch.float16
+
+
+def matmul(a: torch.Tensor, b: torch.Tensor, transpose_a: bool = False,
+           transpose_b: bool = False) -> torch.Tensor:
+    """``_C.matmul``: ``a @ op(b)``.
+
+    The M<=8 fp16 route (the reference's vecmat kernels) runs on this
+    library's kernels; ``b`` is ``[K, N]``, or ``[N, K]`` with ``transpose_b``
+    (the documented contract, include/metal_native/ops/matmul.h:18-37).
+    Shapes outside that route are the reference's non-quantized
+    simd32/tiled64/MPSGraph GEMMs, which this build does not re-implement:
+    they are computed by torch.matmul on the GPU (hipBLASLt).
+    """
+    op = "matmul"
+    if a.dim() < 2:
+        _invalid("matmul: input 'a' must have at least 2 dimensions")
+    if b.dim() < 2:
+        _invalid("matmul: input 'b' must have at least 2 dimensions")
+    if a.dtype != b.dtype:
+        _invalid("matmul: input dtypes must match")
+    _require_cuda(a, "a", op)
+    _require_cuda(b, "b", op)
+    M = a.shape[-1] if transpose_a else a.shape[-2]
+    Ka = a.shape[-2] if transpose_a else a.shape[-1]
+    Kb = b.shape[-1] if transpose_b else b.shape[-2]
+    N = b.shape[-2] if transpose_b else b.shape[-1]
+    if Ka != Kb:
+        _invalid("matmul: incompatible dimensions for matrix multiplication")
+    K = Ka
+    if transpose_a or b.dim() != 2 or not _vecmat_route(M, N, K, a.dtype):
+        aa = a.transpose(-1, -2) if transpose_a else a
+        bb = b.transpose(-1, -2) if transpose_b else b
+        return torch.matmul(aa, bb)
+    lead = a.shape[:-2]
+    a2 = a.reshape(-1, K)
+    if a2.stride(-1) != 1:
+        a2 = a2.contiguous()
+    if b.stride(-1) != 1:
+        b = b.contiguous()
+    rows = a2.shape[0]
+    out = torch.empty((rows, N), dtype=torch.float16, device=a.device)
+    dev = a.device
+    with torch.cuda.device(dev):
+        for r0 in range(0, rows, 64):
+            r1 = min(rows, r0 + 64)
+            ai = a2[r0:r1]
+            need = _L.mq_vecmat_f16_workspace_size(r1 - r0, N, K, 1 if transpose_b else 0)
+            ws, ws_bytes = _workspace(dev, need)
+            rc = _L.mq_vecmat_f16(_ptr(ai), _rows(ai, "a", op), _ptr(b), _rows(b, "b", op),
+                                  _ptr(out[r0:r1]), N, r1 - r0, N, K, 1 if transpose_b else 0,
+                                  _ptr(ws), ws_bytes, _stream_handle(dev))
+            _check(rc)
+    return out.reshape(*lead, M, N)
+
+
+def swiglu(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
+    """``fast.swiglu``: ``half(silu(float(gate)) * float(up))``
+    (src/future/future_stubs.mm:61-101, shaders/fused_swiglu.metal:48-84)."""
+    op = "fast::swiglu"
+    _require_cuda(gate, "gate", op)
+    _require_cuda(up, "up", op)
+    if gate.dtype != up.dtype:
+        _invalid("fast::swiglu: gate and up must have same dtype")
+    if gate.numel() != up.numel():
+        _invalid("fast::swiglu: gate and up must have same number of elements")
+    if gate.dtype != torch.float16:
+        _invalid("fast::swiglu: this build implements Float16")
+    g = gate.contiguous()
+    u = up.contiguous()
+    out = torch.empty_like(g)
+    dev = g.device
+    with torch.cuda.device(dev):
+        rc = _L.mq_swiglu_f16(_ptr(g), _ptr(u), _ptr(out), g.numel(), _stream_handle(dev))
+    _check(rc)
+    return out
+
+
+def synchronize() -> None:
+    """``_C.synchronize``: wait for all queued GPU work."""
+    torch.cuda.synchronize()
+
+
+def set_option(key: str, value: int) -> None:
+    """Kernel-path override for tests/tuning (see mq_set_option)."""
+    _check(_L.mq_set_option(key.encode(), int(value)))
+
+
+def last_path() -> str:
+    return _lib.PATH_NAMES.get(_L.mq_last_path(), "unknown")

@@ -1,0 +1,1 @@
+"""CPU oracle for the quantized-linear path (test infrastructure only)."""

@@ -1,0 +1,117 @@
+"""CPU checks of the C-ABI library: it loads, exports exactly what
+include/metal_native_amd.h declares, and rejects bad arguments before touching
+a GPU (validation mirrors src/ops/matmul.mm:910-934)."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "metal_native_amd.h")
+
+
+def declared():
+    text = open(HEADER).read()
+    return re.findall(r"MQ_API\s+[\w\s\*]+?\b(mq_\w+)\s*\(", text)
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from metal_native import _lib
+
+    return _lib.lib
+
+
+def test_header_declares_entry_points():
+    names = declared()
+    for want in ["mq_dequant_matmul", "mq_dequant_matmul_workspace_size", "mq_dequantize",
+                 "mq_vecmat_f16", "mq_vecmat_f16_workspace_size", "mq_swiglu_f16", "mq_last_error"]:
+        assert want in names
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in declared():
+        assert hasattr(lib, name), name
+    from metal_native import _lib
+
+    assert set(declared()) == set(_lib.SIGNATURES)
+
+
+def test_abi_version_and_error_strings(lib):
+    assert lib.mq_abi_version() == 1
+    assert lib.mq_error_to_string(0) == b"Success"
+    assert lib.mq_error_to_string(4) == b"InvalidArgument"
+    assert lib.mq_error_to_string(8) == b"NotImplemented"
+
+
+def test_validation_without_gpu(lib):
+    P = ctypes.c_void_p(256)  # never dereferenced: validation fails first
+    call = lambda M, N, K, g, qt, epi, ldw=None: lib.mq_dequant_matmul(
+        P, K, P, (K // 2 if qt == 0 else K) if ldw is None else ldw, P, P, P, N, M, N, K, g, qt, epi,
+        None, None, 0, None)
+    assert call(0, 8, 32, 32, 0, 0) == 4
+    assert b"positive" in lib.mq_last_error()
+    assert call(1, 8, 33, 32, 0, 0) == 4  # odd K for int4
+    assert b"INT4 weights must be [N, K/2]" in lib.mq_last_error()
+    assert call(1, 8, 32, 32, 0, 0, ldw=8) == 4
+    assert b"INT4 weights must be [N, K/2]" in lib.mq_last_error()
+    assert call(1, 8, 32, 32, 1, 0, ldw=16) == 4
+    assert b"INT8 weights must be [N, K]" in lib.mq_last_error()
+    assert call(1, 7, 32, 32, 0, 2) == 4  # SwiGLU needs even N
+    assert call(1, 8, 32, 32, 5, 0) == 4
+    assert call(1, 8, 32, 32, 0, 1) == 4  # bias epilogue without bias
+    assert b"bias" in lib.mq_last_error()
+    assert lib.mq_dequantize(P, 16, P, P, P, 32, 4, 32, 32, 0, 1, None) == 4  # flat + zeros
+    assert lib.mq_swiglu_f16(None, P, P, 10, None) == 4
+    assert lib.mq_vecmat_f16(P, 10, P, 10, P, 10, 1, 300, 300, 1, None, 0, None) == 4  # lda < K
+
+
+def test_set_option(lib):
+    assert lib.mq_set_option(b"force_path", 9) == 4
+    assert lib.mq_set_option(b"nonsense", 1) == 4
+    assert b"unknown key" in lib.mq_last_error()
+    assert lib.mq_set_option(b"force_path", 0) == 0
+
+
+def test_python_surface_mirrors_reference():
+    import metal_native as mn
+
+    for name in ("dequant_matmul", "matmul", "synchronize", "MetalNativeError"):
+        assert hasattr(mn._C, name)
+    assert callable(mn._C.fast.swiglu)
+    assert issubclass(mn.MetalNativeError, RuntimeError)
+    from metal_native.ops import quant_type_code
+
+    # bindings/bind_ops.cpp:373: "int4" -> INT4, anything else -> INT8
+    assert quant_type_code("int4") == 0 and quant_type_code("int8") == 1 and quant_type_code("x") == 1
+
+
+def test_python_rejects_cpu_tensors():
+    import torch
+
+    import metal_native as mn
+
+    a = torch.zeros(1, 64, dtype=torch.float16)
+    with pytest.raises(mn.MetalNativeError, match="GPU tensor"):
+        mn.dequant_matmul(a, torch.zeros(8, 32, dtype=torch.uint8), torch.zeros(8, 2, dtype=torch.float16),
+                          torch.zeros(8, 2, dtype=torch.float16), 32, "int4")
+
+
+def test_quantize_matches_oracle_on_cpu():
+    """quantize() is device-agnostic torch code; on CPU tensors it must agree
+    with the oracle's quantizer bit for bit."""
+    import numpy as np
+    import torch
+
+    import metal_native as mn
+    from oracle import mq_oracle as O
+
+    w = (np.random.default_rng(0).standard_normal((12, 256)) * 0.1).astype(np.float16)
+    for qt in ("int4", "int8"):
+        bp, s, z = mn.quantize(torch.from_numpy(w), 64, qt)
+        obp, os_, oz = O.quantize(w, 64, qt)
+        np.testing.assert_array_equal(bp.numpy().view(np.uint8), obp.view(np.uint8))
+        np.testing.assert_array_equal(s.numpy(), os_)
+        np.testing.assert_array_equal(z.numpy(), oz)

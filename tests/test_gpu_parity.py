@@ -1,0 +1,378 @@
+"""GPU parity of the HIP kernels against the CPU oracle (run with -m gpu).
+
+Bars (from the task's contract):
+* dequantized weights: bit-exact;
+* matmul outputs: |y - y_ref| <= 1e-2 + 1e-3 |y_ref| against the oracle's
+  fp32-accumulated result (TOL_ABS / TOL_REL below), every row of A;
+* SwiGLU: the same bound against the oracle's fp16 composition (exp differs
+  by ulps between implementations).
+Every kernel path (skinny split-K MFMA, tiled MFMA, generic) is forced in turn
+on the reference's known-answer cases and on seeded random problems.
+"""
+
+import os
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import mq_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TOL_ABS = 1e-2
+TOL_REL = 1e-3
+GOLD = os.path.join(os.path.dirname(__file__), "golden", "known_answers.npz")
+
+PATHS = {"skinny": 1, "tiled": 2, "generic": 3}
+
+
+@pytest.fixture(scope="module")
+def mn(gpu):
+    import metal_native
+
+    yield metal_native
+    metal_native.set_option("force_path", 0)
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def dev(x, gpu):
+    return torch.from_numpy(np.ascontiguousarray(x)).to(gpu)
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def check_close(y, ref32, what):
+    y = y.astype(np.float64)
+    ref = ref32.astype(np.float64)
+    err = np.abs(y - ref)
+    bound = TOL_ABS + TOL_REL * np.abs(ref)
+    bad = err > bound
+    assert not bad.any(), (f"{what}: {bad.sum()} of {bad.size} outside tolerance; "
+                           f"max abs err {err.max():.3g}, max rel err {(err / np.maximum(np.abs(ref), 1e-6)).max():.3g}")
+
+
+def run_dm(mn, gpu, x, wp, s, z, g, qt, path=None, **kw):
+    mn.set_option("force_path", PATHS[path] if path else 0)
+    try:
+        out = mn.dequant_matmul(dev(x, gpu), dev(wp, gpu), dev(s, gpu), dev(z, gpu), g, qt, **kw)
+        y = host(out)
+        taken = mn.last_path()
+    finally:
+        mn.set_option("force_path", 0)
+    return y, taken
+
+
+def expect_path(path, taken, shape_ok=True):
+    if path and shape_ok:
+        assert taken == path, f"forced {path}, ran {taken}"
+
+
+# ---------------------------------------------------------------------------
+# the reference's known-answer cases
+# ---------------------------------------------------------------------------
+
+def golden_cases():
+    g = np.load(GOLD)
+    return g, sorted({k.split("/")[0] for k in g.files})
+
+
+@pytest.mark.parametrize("path", [None, "skinny", "tiled", "generic"])
+def test_known_answers(mn, gpu, path):
+    gold, names = golden_cases()
+    h = lambda k: gold[k].view(np.float16)
+    for name in names:
+        M, N, K, g, qt = (int(v) for v in gold[f"{name}/meta"])
+        qtype = "int4" if qt == 0 else "int8"
+        say(f"known answer {name} path={path}")
+        y, taken = run_dm(mn, gpu, h(f"{name}/A"), gold[f"{name}/Wp"], h(f"{name}/scales"),
+                          h(f"{name}/zeros"), g, qtype, path)
+        check_close(y, gold[f"{name}/C_exact"], f"{name} [{taken}]")
+        if name == "INT4_SmallKnownAnswer":
+            assert abs(y[0, 0] + 3.3) <= 0.2 and abs(y[0, 1] + 9.0) <= 0.2
+        # dequantized weights bit-exact
+        W = mn.dequantize(dev(gold[f"{name}/Wp"], gpu), dev(h(f"{name}/scales"), gpu),
+                          dev(h(f"{name}/zeros"), gpu), g, qtype, K=K)
+        np.testing.assert_array_equal(host(W).view(np.uint16), gold[f"{name}/W"], err_msg=name)
+
+
+# ---------------------------------------------------------------------------
+# seeded random problems, every path
+# ---------------------------------------------------------------------------
+
+SMALL = [
+    # M, K, N, g
+    (1, 128, 64, 32), (1, 896, 4864, 64), (2, 256, 100, 64), (3, 512, 130, 128), (4, 1024, 64, 128),
+    (7, 384, 200, 32), (8, 2048, 192, 128), (9, 256, 64, 64), (16, 512, 96, 32), (17, 640, 128, 128),
+    (33, 256, 72, 64), (64, 1024, 256, 128), (65, 256, 136, 32), (128, 512, 256, 64), (200, 384, 320, 128),
+]
+
+
+@pytest.mark.parametrize("path", [None, "skinny", "tiled"])
+@pytest.mark.parametrize("M,K,N,g", SMALL)
+def test_int4_random(mn, gpu, path, M, K, N, g):
+    say(f"int4 M={M} K={K} N={N} g={g} path={path}")
+    x, wp, s, z = O.make_int4_problem(M, K, N, g, seed=M * 7 + K + N)
+    ref = O.matmul_f32acc(x, O.dequant_int4(wp, s, z, K, g))
+    y, taken = run_dm(mn, gpu, x, wp, s, z, g, "int4", path)
+    expect_path(path, taken, shape_ok=not (path == "skinny" and M > 64))
+    check_close(y, ref, f"int4 {M}x{K}x{N} g{g} [{taken}]")
+
+
+@pytest.mark.parametrize("path", [None, "skinny", "tiled"])
+@pytest.mark.parametrize("M,K,N", [(1, 256, 64), (4, 512, 96), (16, 1024, 128), (64, 512, 192),
+                                   (100, 256, 160)])
+def test_int8_random(mn, gpu, path, M, K, N):
+    say(f"int8 M={M} K={K} N={N} path={path}")
+    x, q, s, z, g = O.make_int8_problem(M, K, N, seed=M + K + N, g=64)
+    zz = (np.random.default_rng(1).uniform(-0.01, 0.01, s.shape)).astype(np.float16)  # exercise zeros
+    ref = O.matmul_f32acc(x, O.dequant_int8(q, s, zz, K, g))
+    y, taken = run_dm(mn, gpu, x, q, s, zz, g, "int8", path)
+    expect_path(path, taken, shape_ok=not (path == "skinny" and M > 64))
+    check_close(y, ref, f"int8 {M}x{K}x{N} [{taken}]")
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 48, 8), (4, 96, 40), (3, 4, 2), (70, 80, 24), (5, 200, 33)])
+def test_unaligned_shapes(mn, gpu, M, K, N):
+    """K not a multiple of 32 and ragged N: the generic kernel handles them."""
+    say(f"unaligned M={M} K={K} N={N}")
+    x, wp, s, z = O.make_int4_problem(M, K, N, 32, seed=K)
+    ref = O.matmul_f32acc(x, O.dequant_int4(wp, s, z, K, 32))
+    y, taken = run_dm(mn, gpu, x, wp, s, z, 32, "int4")
+    check_close(y, ref, f"unaligned int4 {M}x{K}x{N} [{taken}]")
+
+
+@pytest.mark.parametrize("path", [None, "skinny", "tiled", "generic"])
+@pytest.mark.parametrize("M", [1, 5, 64, 130])
+def test_epilogues(mn, gpu, path, M):
+    say(f"epilogues M={M} path={path}")
+    K, N, g = 512, 256, 64
+    x, wp, s, z = O.make_int4_problem(M, K, N, g, seed=M + 11)
+    acc = O.matmul_f32acc(x, O.dequant_int4(wp, s, z, K, g))
+    b = np.random.default_rng(M).standard_normal(N).astype(np.float16)
+    y, taken = run_dm(mn, gpu, x, wp, s, z, g, "int4", path, epilogue="bias", bias=dev(b, gpu))
+    check_close(y, acc + b.astype(np.float32), f"bias [{taken}]")
+    y, taken = run_dm(mn, gpu, x, wp, s, z, g, "int4", path, epilogue="swiglu")
+    ref = O.apply_epilogue(acc, "swiglu")
+    check_close(y, ref.astype(np.float32), f"swiglu [{taken}]")
+
+
+# ---------------------------------------------------------------------------
+# the benchmark workloads at full size
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("M", [1, 4, 8])
+def test_config2_qwen7b_down(mn, gpu, M):
+    say(f"config2 M={M}")
+    K, N, g = 18944, 3584, 128
+    x, wp, s, z = O.make_int4_problem(M, K, N, g, seed=0)
+    ref = O.matmul_f32acc(x, O.dequant_int4(wp, s, z, K, g))
+    y, taken = run_dm(mn, gpu, x, wp, s, z, g, "int4")
+    assert taken == "skinny"
+    check_close(y, ref, f"config2 M={M}")
+
+
+def test_config1_qwen05b_gate(mn, gpu):
+    say("config1")
+    x, wp, s, z = O.make_int4_problem(1, 896, 4864, 64, seed=0)
+    ref = O.matmul_f32acc(x, O.dequant_int4(wp, s, z, 896, 64))
+    y, _ = run_dm(mn, gpu, x, wp, s, z, 64, "int4")
+    check_close(y, ref, "config1")
+
+
+def test_config3_llama3b_qkv_prefill(mn, gpu):
+    say("config3")
+    M, K, N, g = 512, 3072, 5120, 128
+    x, wp, s, z = O.make_int4_problem(M, K, N, g, seed=0)
+    ref = O.matmul_f32acc(x, O.dequant_int4(wp, s, z, K, g))
+    y, taken = run_dm(mn, gpu, x, wp, s, z, g, "int4")
+    assert taken == "tiled"
+    check_close(y, ref, "config3")
+
+
+@pytest.mark.parametrize("M", [1, 16, 64])
+def test_config4_int8_swiglu(mn, gpu, M):
+    say(f"config4 M={M}")
+    K, F = 3584, 18944
+    x, q, s, z, g = O.make_int8_problem(M, K, 2 * F, seed=0)
+    ref = O.apply_epilogue(O.matmul_f32acc(x, O.dequant_int8(q, s, z, K, g)), "swiglu")
+    y, _ = run_dm(mn, gpu, x, q, s, z, g, "int8", epilogue="swiglu")
+    assert y.shape == (M, F)
+    check_close(y, ref.astype(np.float32), f"config4 M={M}")
+
+
+# ---------------------------------------------------------------------------
+# dequantize, swiglu, vecmat
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("N,K,g,qt", [(3584, 18944, 128, "int4"), (4864, 896, 64, "int4"),
+                                      (37, 96, 32, "int4"), (512, 3584, 3584, "int8"), (33, 48, 32, "int8"),
+                                      (5, 30, 32, "int4")])
+def test_dequantize_bit_exact(mn, gpu, N, K, g, qt):
+    say(f"dequantize N={N} K={K} g={g} {qt}")
+    if qt == "int4":
+        _, wp, s, z = O.make_int4_problem(1, K, N, g, seed=N)
+    else:
+        _, wp, s, z, g = O.make_int8_problem(1, K, N, seed=N, g=g)
+        z = np.random.default_rng(N).uniform(-0.01, 0.01, s.shape).astype(np.float16)
+    want = O.dequantize(wp, s, z, K, g, qt)
+    got = host(mn.dequantize(dev(wp, gpu), dev(s, gpu), dev(z, gpu), g, qt, K=K))
+    np.testing.assert_array_equal(got.view(np.uint16), want.view(np.uint16))
+    got0 = host(mn.dequantize(dev(wp, gpu), dev(s, gpu), None, g, qt, K=K))
+    np.testing.assert_array_equal(got0.view(np.uint16), O.dequantize(wp, s, None, K, g, qt).view(np.uint16))
+
+
+def test_dequantize_special_scales(mn, gpu):
+    """Subnormal, huge (overflowing) and negative scales and zeros: bit-exact."""
+    say("dequantize special scales")
+    rng = np.random.default_rng(5)
+    N, K, g = 64, 256, 32
+    bits = np.array([0x0001, 0x03FF, 0x0400, 0x2E66, 0x3C00, 0x5BFF, 0x7BFF, 0xAE66, 0x8001, 0x0000],
+                    dtype=np.uint16)
+    s = bits[rng.integers(0, len(bits), (N, K // g))].view(np.float16)
+    z = bits[rng.integers(0, len(bits), (N, K // g))].view(np.float16)
+    wp = rng.integers(0, 256, (N, K // 2), dtype=np.uint8)
+    want = O.dequant_int4(wp, s, z, K, g)
+    got = host(mn.dequantize(dev(wp, gpu), dev(s, gpu), dev(z, gpu), g, "int4"))
+    w16, g16 = want.view(np.uint16), got.view(np.uint16)
+    nan_w, nan_g = np.isnan(want), np.isnan(got)
+    np.testing.assert_array_equal(nan_w, nan_g)
+    np.testing.assert_array_equal(w16[~nan_w], g16[~nan_g])
+    q8 = rng.integers(-128, 128, (N, K), dtype=np.int16).astype(np.int8)
+    want8 = O.dequant_int8(q8, s, z, K, g)
+    got8 = host(mn.dequantize(dev(q8, gpu), dev(s, gpu), dev(z, gpu), g, "int8"))
+    nan_w = np.isnan(want8)
+    np.testing.assert_array_equal(nan_w, np.isnan(got8))
+    np.testing.assert_array_equal(want8.view(np.uint16)[~nan_w], got8.view(np.uint16)[~nan_w])
+
+
+@pytest.mark.parametrize("N,K,g,qt", [(64, 128, 32, "int4"), (16, 100, 8, "int4"), (16, 96, 32, "int8"),
+                                      (7, 30, 4, "int8")])
+def test_dequantize_flat_groups(mn, gpu, N, K, g, qt):
+    """Standalone-kernel semantics: flat group index, no zero."""
+    say(f"dequantize flat N={N} K={K} g={g} {qt}")
+    rng = np.random.default_rng(K)
+    nsc = (N * K + g - 1) // g
+    s = rng.uniform(0.005, 0.02, (nsc,)).astype(np.float16)
+    if qt == "int4":
+        wp = rng.integers(0, 256, (N, K // 2), dtype=np.uint8)
+    else:
+        wp = rng.integers(-128, 128, (N, K), dtype=np.int16).astype(np.int8)
+    want = O.dequantize_flat(wp, s, N * K, g, qt).reshape(N, K)
+    got = host(mn.dequantize(dev(wp, gpu), dev(s, gpu), None, g, qt, K=K, flat_groups=True))
+    np.testing.assert_array_equal(got.view(np.uint16), want.view(np.uint16))
+
+
+@pytest.mark.parametrize("n", [1, 7, 8, 1000, 18944 * 16 + 3])
+def test_swiglu_op(mn, gpu, n):
+    say(f"swiglu n={n}")
+    rng = np.random.default_rng(n)
+    g = (rng.standard_normal(n) * 4).astype(np.float16)
+    u = rng.standard_normal(n).astype(np.float16)
+    got = host(mn.fast.swiglu(dev(g, gpu), dev(u, gpu)))
+    check_close(got, O.swiglu(g, u).astype(np.float32), "swiglu")
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 256, 256), (1, 4096, 4096), (4, 896, 4864), (8, 1000, 300),
+                                   (3, 260, 257)])
+@pytest.mark.parametrize("transpose_b", [True, False])
+def test_vecmat_route(mn, gpu, M, K, N, transpose_b):
+    say(f"vecmat M={M} K={K} N={N} tb={transpose_b}")
+    rng = np.random.default_rng(M * K + N)
+    a = rng.standard_normal((M, K)).astype(np.float16)
+    b = (rng.standard_normal((N, K) if transpose_b else (K, N)) * 0.05).astype(np.float16)
+    got = host(mn.matmul(dev(a, gpu), dev(b, gpu), False, transpose_b))
+    ref = a.astype(np.float32) @ (b.T if transpose_b else b).astype(np.float32)
+    assert mn.last_path() in ("skinny", "vecmat_kn", "generic")
+    check_close(got, ref, f"vecmat tb={transpose_b}")
+
+
+# ---------------------------------------------------------------------------
+# behaviour: determinism, row independence, workspace reuse, graphs, errors
+# ---------------------------------------------------------------------------
+
+def test_split_k_is_deterministic(mn, gpu):
+    say("determinism")
+    x, wp, s, z = O.make_int4_problem(8, 18944, 3584, 128, seed=1)
+    args = [dev(v, gpu) for v in (x, wp, s, z)]
+    y0 = host(mn.dequant_matmul(*args, 128, "int4"))
+    for _ in range(3):
+        np.testing.assert_array_equal(host(mn.dequant_matmul(*args, 128, "int4")).view(np.uint16),
+                                      y0.view(np.uint16))
+
+
+def test_rows_are_independent(mn, gpu):
+    """Every row of A is computed (the reference's M<=8 kernel fills row 0 only)."""
+    say("row independence")
+    x, wp, s, z = O.make_int4_problem(8, 4096, 512, 128, seed=2)
+    W = [dev(v, gpu) for v in (wp, s, z)]
+    y8 = host(mn.dequant_matmul(dev(x, gpu), *W, 128, "int4"))
+    for m in range(8):
+        y1 = host(mn.dequant_matmul(dev(x[m:m + 1], gpu), *W, 128, "int4"))
+        np.testing.assert_allclose(y1[0].astype(np.float32), y8[m].astype(np.float32), atol=2e-3, rtol=2e-3)
+    assert np.abs(y8[1:] - y8[:1]).max() > 0
+
+
+def test_workspace_reuse_across_shapes(mn, gpu):
+    say("workspace reuse")
+    probs = [O.make_int4_problem(M, K, N, 128, seed=M + K) for M, K, N in
+             [(1, 8192, 1024), (8, 4096, 2048), (3, 16384, 512), (1, 8192, 1024)]]
+    refs = [O.matmul_f32acc(x, O.dequant_int4(wp, s, z, x.shape[1], 128)) for x, wp, s, z in probs]
+    for rep in range(2):
+        outs = [mn.dequant_matmul(*[dev(v, gpu) for v in p], 128, "int4") for p in probs]
+        for o, r in zip(outs, refs):
+            check_close(host(o), r, f"reuse rep {rep}")
+
+
+def test_hip_graph_replay(mn, gpu):
+    """Capture the decode GEMV (split-K with its counters) in a HIP graph and
+    replay it several times with eager work in between."""
+    say("graph replay")
+    x, wp, s, z = O.make_int4_problem(4, 18944, 3584, 128, seed=3)
+    xa, wa, sa, za = (dev(v, gpu) for v in (x, wp, s, z))
+    eager = host(mn.dequant_matmul(xa, wa, sa, za, 128, "int4"))
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        mn.dequant_matmul(xa, wa, sa, za, 128, "int4")  # allocate this stream's workspace
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        out = mn.dequant_matmul(xa, wa, sa, za, 128, "int4")
+    for rep in range(4):
+        graph.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(out.cpu().numpy().view(np.uint16), eager.view(np.uint16),
+                                      err_msg=f"replay {rep}")
+        _ = host(mn.dequant_matmul(xa[:1].contiguous(), wa, sa, za, 128, "int4"))  # eager work between
+
+
+def test_errors_on_gpu_tensors(mn, gpu):
+    say("errors")
+    x = torch.zeros(2, 64, dtype=torch.float16, device=gpu)
+    wp = torch.zeros(8, 32, dtype=torch.uint8, device=gpu)
+    s = torch.zeros(8, 2, dtype=torch.float16, device=gpu)
+    with pytest.raises(mn.MetalNativeError, match="activations must be 2D"):
+        mn.dequant_matmul(x[None], wp, s, s, 32, "int4")
+    with pytest.raises(mn.MetalNativeError, match="activations must be Float16"):
+        mn.dequant_matmul(x.float(), wp, s, s, 32, "int4")
+    with pytest.raises(mn.MetalNativeError, match="group_size must be 32, 64, or 128"):
+        mn.dequant_matmul(x, wp, s, s, 16, "int4")
+    with pytest.raises(mn.MetalNativeError, match=r"INT4 weights must be \[N, K/2\]"):
+        mn.dequant_matmul(x, wp[:, :16], s, s, 32, "int4")
+    with pytest.raises(mn.MetalNativeError, match=r"INT8 weights must be \[N, K\]"):
+        mn.dequant_matmul(x, wp, s, s, 32, "int8")
+    with pytest.raises(mn.MetalNativeError, match="scales must be"):
+        mn.dequant_matmul(x, wp, s[:, :1], s, 32, "int4")
+    # any quant_type other than "int4" is INT8 (bindings/bind_ops.cpp:373)
+    w8 = torch.zeros(8, 64, dtype=torch.int8, device=gpu)
+    assert mn.dequant_matmul(x, w8, s, s, 32, "whatever").shape == (2, 8)
