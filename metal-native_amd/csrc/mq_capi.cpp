@@ -17,6 +17,10 @@ thread_local std::string g_last_error;
 thread_local int g_last_path = 0;
 std::atomic<int> g_force_path{0};
 std::atomic<int> g_wg_per_cu{4};
+std::atomic<int> g_splitk_nofence{0};
+std::atomic<int> g_gemv_max_nw{16};
+std::atomic<int> g_gemv_xfull{1};
+std::atomic<int> g_gemv_rpw{0};
 
 int fail(int code, const std::string& msg) {
   g_last_error = msg;
@@ -41,26 +45,37 @@ int num_cus_current() {
   return cache[dev];
 }
 
-enum Path { PATH_AUTO = 0, PATH_SKINNY = 1, PATH_TILED = 2, PATH_GENERIC = 3, PATH_VECMAT_KN = 4 };
+enum Path {
+  PATH_AUTO = 0, PATH_SPLITK = 1, PATH_TILED = 2, PATH_GENERIC = 3, PATH_VECMAT_KN = 4, PATH_GEMV = 5
+};
 
 int choose_path(const mq::LinearArgs& a) {
   int forced = g_force_path.load();
-  if (forced == PATH_SKINNY && mq::skinny_supported(a)) return PATH_SKINNY;
+  if (forced == PATH_SPLITK && mq::skinny_supported(a)) return PATH_SPLITK;
+  if (forced == PATH_GEMV && mq::gemv_supported(a)) return PATH_GEMV;
   if (forced == PATH_TILED && mq::tiled_supported(a)) return PATH_TILED;
   if (forced == PATH_GENERIC) return PATH_GENERIC;
-  if (a.M <= 64 && mq::skinny_supported(a)) return PATH_SKINNY;
+  if (a.M <= 64 && mq::gemv_supported(a)) return PATH_GEMV;
   if (mq::tiled_supported(a)) return PATH_TILED;
   return PATH_GENERIC;
 }
 
 mq::SkinnyPlan plan_for(const mq::LinearArgs& a) {
-  return mq::skinny_plan(a, num_cus_current() * g_wg_per_cu.load() / 4, 0);
+  mq::SkinnyPlan p = mq::skinny_plan(a, num_cus_current() * g_wg_per_cu.load() / 4, 0);
+  p.nofence = g_splitk_nofence.load();
+  return p;
 }
 
 int run_linear(const mq::LinearArgs& a, void* ws, size_t ws_bytes, hipStream_t s) {
   int path = choose_path(a);
   hipError_t e;
-  if (path == PATH_SKINNY) {
+  if (path == PATH_GEMV) {
+    mq::GemvTuning t;
+    t.allow_full = g_gemv_xfull.load() != 0;
+    t.max_nw = g_gemv_max_nw.load();
+    t.rpw = g_gemv_rpw.load();
+    e = mq::gemv_launch(a, mq::gemv_plan(a, t), s);
+  } else if (path == PATH_SPLITK) {
     mq::SkinnyPlan p = plan_for(a);
     if (p.ws_bytes > 0 && (ws == nullptr || ws_bytes < p.ws_bytes))
       return fail(MQ_INVALID_ARGUMENT, "dequant_matmul: workspace too small (need " +
@@ -145,7 +160,7 @@ MQ_API size_t mq_dequant_matmul_workspace_size(int64_t M, int64_t N, int64_t K, 
   a.lda = K; a.ldw = quant_type == MQ_QUANT_INT4 ? K / 2 : K; a.ldc = N;
   a.A = (const void*)256; a.W = (const void*)256;
   if (a.ldw & 15) return 0;
-  if (choose_path(a) != PATH_SKINNY) return 0;
+  if (choose_path(a) != PATH_SPLITK) return 0;
   return plan_for(a).ws_bytes;
 }
 
@@ -204,7 +219,8 @@ MQ_API int mq_vecmat_f16(const void* a, int64_t lda, const void* b, int64_t ldb,
   la.epi = mq::EPI_NONE;
   int path = choose_path(la);
   if (path == PATH_TILED) path = PATH_GENERIC;  // the tiled kernel takes quantized weights only
-  if (path == PATH_SKINNY) return run_linear(la, workspace, workspace_bytes, (hipStream_t)stream);
+  if (path == PATH_GEMV || path == PATH_SPLITK)
+    return run_linear(la, workspace, workspace_bytes, (hipStream_t)stream);
   hipError_t e = mq::generic_linear_launch(la, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "matmul: kernel launch failed");
   g_last_path = PATH_GENERIC;
@@ -222,7 +238,7 @@ MQ_API size_t mq_vecmat_f16_workspace_size(int64_t M, int64_t N, int64_t K, int3
   la.fmt = mq::FMT_F16;
   la.epi = mq::EPI_NONE;
   if (la.ldw & 15) return 0;
-  if (choose_path(la) != PATH_SKINNY) return 0;
+  if (choose_path(la) != PATH_SPLITK) return 0;
   return plan_for(la).ws_bytes;
 }
 
@@ -238,13 +254,34 @@ MQ_API int mq_swiglu_f16(const void* gate, const void* up, void* out, int64_t n,
 MQ_API int mq_set_option(const char* key, int64_t value) {
   if (!key) return fail(MQ_INVALID_ARGUMENT, "set_option: null key");
   if (std::strcmp(key, "force_path") == 0) {
-    if (value < 0 || value > 3) return fail(MQ_INVALID_ARGUMENT, "set_option: force_path must be 0..3");
+    if (value < 0 || value > 5 || value == PATH_VECMAT_KN)
+      return fail(MQ_INVALID_ARGUMENT, "set_option: force_path must be 0, 1, 2, 3 or 5");
     g_force_path.store((int)value);
     return MQ_SUCCESS;
   }
   if (std::strcmp(key, "skinny_wg_per_cu") == 0) {
     if (value < 1 || value > 64) return fail(MQ_INVALID_ARGUMENT, "set_option: skinny_wg_per_cu must be 1..64");
     g_wg_per_cu.store((int)value);
+    return MQ_SUCCESS;
+  }
+  if (std::strcmp(key, "splitk_nofence") == 0) {  // timing experiments only: results are not valid
+    g_splitk_nofence.store(value ? 1 : 0);
+    return MQ_SUCCESS;
+  }
+  if (std::strcmp(key, "gemv_xfull") == 0) {
+    g_gemv_xfull.store(value ? 1 : 0);
+    return MQ_SUCCESS;
+  }
+  if (std::strcmp(key, "gemv_rpw") == 0) {
+    if (value != 0 && value != 2 && value != 4 && value != 8 && value != 16)
+      return fail(MQ_INVALID_ARGUMENT, "set_option: gemv_rpw must be 0, 2, 4, 8 or 16");
+    g_gemv_rpw.store((int)value);
+    return MQ_SUCCESS;
+  }
+  if (std::strcmp(key, "gemv_max_nw") == 0) {
+    if (value != 2 && value != 4 && value != 8 && value != 16)
+      return fail(MQ_INVALID_ARGUMENT, "set_option: gemv_max_nw must be 2, 4, 8 or 16");
+    g_gemv_max_nw.store((int)value);
     return MQ_SUCCESS;
   }
   return fail(MQ_INVALID_ARGUMENT, std::string("set_option: unknown key ") + key);

@@ -71,6 +71,30 @@ __device__ __forceinline__ h8 dq_int4_dword_perm(uint32_t d, h2 s, h2 z) {
   return r;
 }
 
+// Same as dq_int4_dword_perm with the masks and the 0x6400 pair passed in as
+// values: kept in registers they let the compiler emit one v_and_or_b32 per
+// nibble pair instead of an AND and an OR with literal operands.
+// (d & mask) | magic in one VALU op; mask lives in a VGPR and magic in an SGPR
+// (gfx9 VOP3 encodings take one scalar operand and no literal).
+__device__ __forceinline__ uint32_t and_or(uint32_t d, uint32_t mask_v, uint32_t magic_s) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(d), "v"(mask_v), "s"(magic_s));
+  return r;
+}
+__device__ __forceinline__ h8 dq_int4_dword_perm_r(uint32_t d, h2 s, h2 z, uint32_t mlo, uint32_t mhi,
+                                                   uint32_t magic) {
+  const uint32_t d8 = d >> 8;
+  const h2 c1032 = (h2){(_Float16)1032.0f, (_Float16)1032.0f};
+  const h2 c16 = (h2){(_Float16)0.0625f, (_Float16)0.0625f};
+  const h2 c72 = (h2){(_Float16)-72.0f, (_Float16)-72.0f};
+  h8 r;
+  r.s01 = scale_sub(as_h2(and_or(d, mlo, magic)) - c1032, s, z);                                // k0, k4
+  r.s23 = scale_sub(__builtin_elementwise_fma(as_h2(and_or(d, mhi, magic)), c16, c72), s, z);   // k1, k5
+  r.s45 = scale_sub(as_h2(and_or(d8, mlo, magic)) - c1032, s, z);                               // k2, k6
+  r.s67 = scale_sub(__builtin_elementwise_fma(as_h2(and_or(d8, mhi, magic)), c16, c72), s, z);  // k3, k7
+  return r;
+}
+
 // Eight int4 weights in natural k order (used where the output is stored,
 // i.e. the dequantize op).  v_perm_b32 copies byte b into bytes 0 and 2 so
 // the two nibbles of one byte land in the two fp16 halves.

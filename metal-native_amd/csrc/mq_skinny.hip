@@ -37,6 +37,7 @@ struct SkinnyKArgs {
   int M, N, K, g, G, F;
   int gshift;           // log2(g) when g is a power of two, else -1
   int splits;
+  int nofence;          // timing experiments only: drop the release/acquire fences
   uint32_t* counters;   // [rblocks]
   float* partials;      // [splits, M, N]
 };
@@ -168,7 +169,7 @@ __global__ __launch_bounds__(kThreads) void skinny_kernel(SkinnyKArgs p) {
           if (m < p.M) p.partials[((int64_t)sidx * p.M + m) * p.N + n] = acc[mb][r];
         }
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    if (!p.nofence) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
     __syncthreads();
     if (tid == 0) {
       uint32_t prev = __hip_atomic_fetch_add(p.counters + rb, 1u, __ATOMIC_ACQ_REL,
@@ -177,7 +178,7 @@ __global__ __launch_bounds__(kThreads) void skinny_kernel(SkinnyKArgs p) {
     }
     __syncthreads();
     if (!s_last) return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    if (!p.nofence) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     for (int idx = tid; idx < p.M * 64; idx += kThreads) {
       int m = idx >> 6, c = idx & 63;
       int nn;
@@ -272,6 +273,8 @@ bool skinny_supported(const LinearArgs& a) {
   if (((uintptr_t)a.W & 15) || (a.ldw & 15)) return false;
   if (((uintptr_t)a.A & 15) || (a.lda & 7)) return false;
   if (a.epi == EPI_SWIGLU && a.F * 2 != a.N) return false;
+  const int64_t rblocks = (a.epi == EPI_SWIGLU) ? (a.F + 31) / 32 : (a.N + kRowsPerBlock - 1) / kRowsPerBlock;
+  if (rblocks * 4 > (int64_t)kWsCounterBytes) return false;  // one counter per row block
   return true;
 }
 
@@ -294,8 +297,7 @@ SkinnyPlan skinny_plan(const LinearArgs& a, int num_cus, size_t ws_avail) {
   p.steps = steps;
   p.kchunk = steps * kstep;
   p.splits = (a.K + p.kchunk - 1) / p.kchunk;
-  size_t cnt_bytes = ((size_t)p.rblocks * 4 + 255) & ~(size_t)255;
-  p.ws_bytes = p.splits > 1 ? cnt_bytes + (size_t)p.splits * a.M * a.N * 4 : 0;
+  p.ws_bytes = p.splits > 1 ? kWsCounterBytes + (size_t)p.splits * a.M * a.N * 4 : 0;
   (void)ws_avail;
   p.lds_bytes = (size_t)a.M * (p.kchunk + 8) * 2 + (size_t)a.M * 64 * 4;
   return p;
@@ -310,13 +312,13 @@ hipError_t skinny_launch(const LinearArgs& a, const SkinnyPlan& p, void* ws, hip
   k.C = (_Float16*)a.C; k.ldc = a.ldc;
   k.M = a.M; k.N = a.N; k.K = a.K; k.g = a.g > 0 ? a.g : 1; k.G = a.G; k.F = a.F;
   k.splits = p.splits;
+  k.nofence = p.nofence;
   k.gshift = -1;
   for (int b = 0; b < 31; ++b)
     if (k.g == (1 << b)) k.gshift = b;
   if (p.splits > 1) {
-    size_t cnt_bytes = ((size_t)p.rblocks * 4 + 255) & ~(size_t)255;
     k.counters = (uint32_t*)ws;
-    k.partials = (float*)((char*)ws + cnt_bytes);
+    k.partials = (float*)((char*)ws + kWsCounterBytes);
   }
   switch (a.fmt) {
     case FMT_INT4: return by_steps<FMT_INT4>(p, a.epi, k, s);

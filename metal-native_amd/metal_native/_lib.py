@@ -27,7 +27,7 @@ EPILOGUE_NONE = 0
 EPILOGUE_BIAS = 1
 EPILOGUE_SWIGLU = 2
 
-PATH_NAMES = {0: "none", 1: "skinny", 2: "tiled", 3: "generic", 4: "vecmat_kn"}
+PATH_NAMES = {0: "none", 1: "splitk", 2: "tiled", 3: "generic", 4: "vecmat_kn", 5: "gemv"}
 
 _c_void_p = ctypes.c_void_p
 _i64 = ctypes.c_int64

@@ -25,7 +25,7 @@ TOL_ABS = 1e-2
 TOL_REL = 1e-3
 GOLD = os.path.join(os.path.dirname(__file__), "golden", "known_answers.npz")
 
-PATHS = {"skinny": 1, "tiled": 2, "generic": 3}
+PATHS = {"splitk": 1, "tiled": 2, "generic": 3, "gemv": 5}
 
 
 @pytest.fixture(scope="module")
@@ -60,6 +60,29 @@ def check_close(y, ref32, what):
                            f"max abs err {err.max():.3g}, max rel err {(err / np.maximum(np.abs(ref), 1e-6)).max():.3g}")
 
 
+def check_swiglu(y, acc, what):
+    """SwiGLU outputs against the oracle's composition half(silu(half(g)) * half(u)).
+
+    The gate and up projections are rounded to fp16 before the SwiGLU (as in
+    the reference's two-dispatch composition), so a one-ulp flip of that
+    rounding -- which any change of fp32 summation order can cause -- moves
+    the output by |d out/d g| * ulp(g) or |silu(g)| * ulp(u).  The bound is the
+    matmul tolerance plus exactly that sensitivity to one flip of each."""
+    F = acc.shape[1] // 2
+    g = acc[:, :F].astype(np.float16)
+    u = acc[:, F:].astype(np.float16)
+    ref = O.swiglu(g, u).astype(np.float64)
+    gd, ud = g.astype(np.float64), u.astype(np.float64)
+    sig = 1.0 / (1.0 + np.exp(-gd))
+    dsilu = sig * (1.0 + gd * (1.0 - sig))
+    ulp = lambda v: np.spacing(np.abs(v)).astype(np.float64)
+    bound = (TOL_ABS + TOL_REL * np.abs(ref) + np.abs(dsilu * ud) * ulp(g) + np.abs(gd * sig) * ulp(u))
+    err = np.abs(y.astype(np.float64) - ref)
+    bad = err > bound
+    assert not bad.any(), (f"{what}: {bad.sum()} of {bad.size} outside the SwiGLU bound; "
+                           f"max abs err {err.max():.3g}")
+
+
 def run_dm(mn, gpu, x, wp, s, z, g, qt, path=None, **kw):
     mn.set_option("force_path", PATHS[path] if path else 0)
     try:
@@ -85,7 +108,7 @@ def golden_cases():
     return g, sorted({k.split("/")[0] for k in g.files})
 
 
-@pytest.mark.parametrize("path", [None, "skinny", "tiled", "generic"])
+@pytest.mark.parametrize("path", [None, "gemv", "splitk", "tiled", "generic"])
 def test_known_answers(mn, gpu, path):
     gold, names = golden_cases()
     h = lambda k: gold[k].view(np.float16)
@@ -116,18 +139,18 @@ SMALL = [
 ]
 
 
-@pytest.mark.parametrize("path", [None, "skinny", "tiled"])
+@pytest.mark.parametrize("path", [None, "gemv", "splitk", "tiled"])
 @pytest.mark.parametrize("M,K,N,g", SMALL)
 def test_int4_random(mn, gpu, path, M, K, N, g):
     say(f"int4 M={M} K={K} N={N} g={g} path={path}")
     x, wp, s, z = O.make_int4_problem(M, K, N, g, seed=M * 7 + K + N)
     ref = O.matmul_f32acc(x, O.dequant_int4(wp, s, z, K, g))
     y, taken = run_dm(mn, gpu, x, wp, s, z, g, "int4", path)
-    expect_path(path, taken, shape_ok=not (path == "skinny" and M > 64))
+    expect_path(path, taken, shape_ok=not (path in ("gemv", "splitk") and M > 64))
     check_close(y, ref, f"int4 {M}x{K}x{N} g{g} [{taken}]")
 
 
-@pytest.mark.parametrize("path", [None, "skinny", "tiled"])
+@pytest.mark.parametrize("path", [None, "gemv", "splitk", "tiled"])
 @pytest.mark.parametrize("M,K,N", [(1, 256, 64), (4, 512, 96), (16, 1024, 128), (64, 512, 192),
                                    (100, 256, 160)])
 def test_int8_random(mn, gpu, path, M, K, N):
@@ -136,7 +159,7 @@ def test_int8_random(mn, gpu, path, M, K, N):
     zz = (np.random.default_rng(1).uniform(-0.01, 0.01, s.shape)).astype(np.float16)  # exercise zeros
     ref = O.matmul_f32acc(x, O.dequant_int8(q, s, zz, K, g))
     y, taken = run_dm(mn, gpu, x, q, s, zz, g, "int8", path)
-    expect_path(path, taken, shape_ok=not (path == "skinny" and M > 64))
+    expect_path(path, taken, shape_ok=not (path in ("gemv", "splitk") and M > 64))
     check_close(y, ref, f"int8 {M}x{K}x{N} [{taken}]")
 
 
@@ -150,7 +173,7 @@ def test_unaligned_shapes(mn, gpu, M, K, N):
     check_close(y, ref, f"unaligned int4 {M}x{K}x{N} [{taken}]")
 
 
-@pytest.mark.parametrize("path", [None, "skinny", "tiled", "generic"])
+@pytest.mark.parametrize("path", [None, "gemv", "splitk", "tiled", "generic"])
 @pytest.mark.parametrize("M", [1, 5, 64, 130])
 def test_epilogues(mn, gpu, path, M):
     say(f"epilogues M={M} path={path}")
@@ -161,8 +184,7 @@ def test_epilogues(mn, gpu, path, M):
     y, taken = run_dm(mn, gpu, x, wp, s, z, g, "int4", path, epilogue="bias", bias=dev(b, gpu))
     check_close(y, acc + b.astype(np.float32), f"bias [{taken}]")
     y, taken = run_dm(mn, gpu, x, wp, s, z, g, "int4", path, epilogue="swiglu")
-    ref = O.apply_epilogue(acc, "swiglu")
-    check_close(y, ref.astype(np.float32), f"swiglu [{taken}]")
+    check_swiglu(y, acc, f"swiglu [{taken}]")
 
 
 # ---------------------------------------------------------------------------
@@ -175,9 +197,10 @@ def test_config2_qwen7b_down(mn, gpu, M):
     K, N, g = 18944, 3584, 128
     x, wp, s, z = O.make_int4_problem(M, K, N, g, seed=0)
     ref = O.matmul_f32acc(x, O.dequant_int4(wp, s, z, K, g))
-    y, taken = run_dm(mn, gpu, x, wp, s, z, g, "int4")
-    assert taken == "skinny"
-    check_close(y, ref, f"config2 M={M}")
+    for path in ("gemv", "splitk"):
+        y, taken = run_dm(mn, gpu, x, wp, s, z, g, "int4", path)
+        assert taken == path
+        check_close(y, ref, f"config2 M={M} [{path}]")
 
 
 def test_config1_qwen05b_gate(mn, gpu):
@@ -203,10 +226,11 @@ def test_config4_int8_swiglu(mn, gpu, M):
     say(f"config4 M={M}")
     K, F = 3584, 18944
     x, q, s, z, g = O.make_int8_problem(M, K, 2 * F, seed=0)
-    ref = O.apply_epilogue(O.matmul_f32acc(x, O.dequant_int8(q, s, z, K, g)), "swiglu")
-    y, _ = run_dm(mn, gpu, x, q, s, z, g, "int8", epilogue="swiglu")
-    assert y.shape == (M, F)
-    check_close(y, ref.astype(np.float32), f"config4 M={M}")
+    acc = O.matmul_f32acc(x, O.dequant_int8(q, s, z, K, g))
+    for path in ("gemv", "splitk"):
+        y, taken = run_dm(mn, gpu, x, q, s, z, g, "int8", path, epilogue="swiglu")
+        assert y.shape == (M, F) and taken == path
+        check_swiglu(y, acc, f"config4 M={M} [{path}]")
 
 
 # ---------------------------------------------------------------------------
@@ -291,7 +315,7 @@ def test_vecmat_route(mn, gpu, M, K, N, transpose_b):
     b = (rng.standard_normal((N, K) if transpose_b else (K, N)) * 0.05).astype(np.float16)
     got = host(mn.matmul(dev(a, gpu), dev(b, gpu), False, transpose_b))
     ref = a.astype(np.float32) @ (b.T if transpose_b else b).astype(np.float32)
-    assert mn.last_path() in ("skinny", "vecmat_kn", "generic")
+    assert mn.last_path() in ("gemv", "vecmat_kn", "generic")
     check_close(got, ref, f"vecmat tb={transpose_b}")
 
 
@@ -376,3 +400,31 @@ def test_errors_on_gpu_tensors(mn, gpu):
     # any quant_type other than "int4" is INT8 (bindings/bind_ops.cpp:373)
     w8 = torch.zeros(8, 64, dtype=torch.int8, device=gpu)
     assert mn.dequant_matmul(x, w8, s, s, 32, "whatever").shape == (2, 8)
+
+
+@pytest.mark.parametrize("rpw", [2, 4, 8, 16])
+@pytest.mark.parametrize("max_nw", [8, 16])
+@pytest.mark.parametrize("M,K,N,g,qt", [(1, 18944, 512, 128, "int4"), (3, 4096, 200, 64, "int4"),
+                                        (4, 896, 4864, 64, "int4"), (2, 3584, 256, 3584, "int8"),
+                                        (8, 2304, 96, 32, "int4"), (1, 1008, 70, 1008, "int8"),
+                                        (2, 18944, 3584, 128, "int4")])
+def test_gemv_variants(mn, gpu, rpw, max_nw, M, K, N, g, qt):
+    """Every whole-K GEMV layout (rows per workgroup x K shifts) and workgroup
+    width against the oracle, including a K that is not a multiple of the step
+    and a group size that forces the generic kernel."""
+    say(f"gemv variant rpw={rpw} nw<={max_nw} M={M} K={K} N={N} g={g} {qt}")
+    if qt == "int4":
+        x, wp, s, z = O.make_int4_problem(M, K, N, g, seed=K + N)
+        ref = O.matmul_f32acc(x, O.dequant_int4(wp, s, z, K, g))
+    else:
+        x, wp, s, z, g = O.make_int8_problem(M, K, N, seed=K + N, g=g)
+        ref = O.matmul_f32acc(x, O.dequant_int8(wp, s, z, K, g))
+    mn.set_option("gemv_rpw", rpw)
+    mn.set_option("gemv_max_nw", max_nw)
+    try:
+        y, taken = run_dm(mn, gpu, x, wp, s, z, g, qt)
+    finally:
+        mn.set_option("gemv_rpw", 0)
+        mn.set_option("gemv_max_nw", 16)
+    assert taken == "gemv"
+    check_close(y, ref, f"gemv rpw={rpw} [{taken}]")
