@@ -207,6 +207,27 @@ def cpu_baseline(reps: int = 3):
     }
 
 
+def copy_calibration(device, nbytes: int = 2**30, reps: int = 20):
+    """A plain copy of known size (nbytes read + nbytes written per launch):
+    the FETCH_SIZE / WRITE_SIZE counters of this kernel give the scale factor
+    from counter units to bytes."""
+    import torch
+
+    src = torch.empty(nbytes, dtype=torch.uint8, device=device).fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize(device)
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    t1.record()
+    torch.cuda.synchronize(device)
+    us = t0.elapsed_time(t1) * 1000.0 / reps
+    print(json.dumps({"copy_bytes_read": nbytes, "copy_bytes_written": nbytes, "us_per_copy": round(us, 2),
+                      "GB/s_read+write": round(2 * nbytes / (us * 1e-6) / 1e9, 1)}), flush=True)
+
+
 # --------------------------------------------------------------------------
 
 def main():
@@ -217,6 +238,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-reps", type=int, default=3)
     ap.add_argument("--only", default=None, help="comma-separated config names (headline always runs)")
+    ap.add_argument("--copy-calib", action="store_true",
+                    help="only run a plain 1 GiB device-to-device copy (rocprof counter calibration)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -232,6 +255,9 @@ def main():
     import metal_native  # noqa: F401  (fails loudly if the library is not built)
 
     device = torch.device("cuda:0")
+    if args.copy_calib:
+        copy_calibration(device)
+        return
     names = list(CONFIGS)
     if args.only:
         want = set(args.only.split(",")) | {HEADLINE}

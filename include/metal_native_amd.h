@@ -59,20 +59,12 @@ enum mq_epilogue { MQ_EPILOGUE_NONE = 0, MQ_EPILOGUE_BIAS = 1, MQ_EPILOGUE_SWIGL
  * src/ops/matmul.mm:903-1029; bound as _C.dequant_matmul at
  * bindings/bind_ops.cpp:366-382).  Strides are in elements for A/out and in
  * bytes for the weights (ldw_bytes; K/2 for packed int4 rows, K for int8).
- * workspace: device memory of at least mq_dequant_matmul_workspace_size()
- * bytes whose first 256-byte-aligned counter region is zero before the first
- * call; every call leaves it zero again.  Calls that share a workspace must be
- * ordered on one stream.  May be NULL when the size query returns 0. */
+ * zeros may be NULL (no zero term); bias is read only for MQ_EPILOGUE_BIAS.
+ * The kernels use no memory beyond the arguments. */
 MQ_API int mq_dequant_matmul(const void* activations, int64_t lda, const void* weights_packed,
                              int64_t ldw_bytes, const void* scales, const void* zeros, void* out,
                              int64_t ldc, int64_t M, int64_t N, int64_t K, int32_t group_size,
-                             int32_t quant_type, int32_t epilogue, const void* bias, void* workspace,
-                             size_t workspace_bytes, void* stream);
-
-/* Workspace bytes mq_dequant_matmul needs for this problem on the current
- * device (0 when no split-K combine is used). */
-MQ_API size_t mq_dequant_matmul_workspace_size(int64_t M, int64_t N, int64_t K, int32_t group_size,
-                                               int32_t quant_type, int32_t epilogue);
+                             int32_t quant_type, int32_t epilogue, const void* bias, void* stream);
 
 /* Dequantize to fp16 out[N, K] (row stride ldo elements).
  * flat_groups == 0: per-row groups scales[n, k/g], optional zeros (NULL = no
@@ -89,26 +81,25 @@ MQ_API int mq_dequantize(const void* weights_packed, int64_t ldw_bytes, const vo
  * transpose_b != 0: B is [N, K] (nn.Linear weight, python/metal_native/nn/linear.py:47-49);
  * transpose_b == 0: B is [K, N].  Replaces matmul_vecmat
  * (src/ops/matmul.mm:192-298, shaders/matmul_vecmat_kernel.metal:32-456) following
- * the documented contract C = A @ op(B) (include/metal_native/ops/matmul.h:18-37).
- * workspace as for mq_dequant_matmul (size from mq_vecmat_f16_workspace_size). */
+ * the documented contract C = A @ op(B) (include/metal_native/ops/matmul.h:18-37). */
 MQ_API int mq_vecmat_f16(const void* a, int64_t lda, const void* b, int64_t ldb, void* c, int64_t ldc,
-                         int64_t M, int64_t N, int64_t K, int32_t transpose_b, void* workspace,
-                         size_t workspace_bytes, void* stream);
-MQ_API size_t mq_vecmat_f16_workspace_size(int64_t M, int64_t N, int64_t K, int32_t transpose_b);
+                         int64_t M, int64_t N, int64_t K, int32_t transpose_b, void* stream);
 
 /* out[i] = half(silu(float(gate[i])) * float(up[i])), i < n.
  * Replaces fast::swiglu (src/future/future_stubs.mm:61-101, bound as
  * _C.fast.swiglu at bindings/bind_ops.cpp:84-93). */
 MQ_API int mq_swiglu_f16(const void* gate, const void* up, void* out, int64_t n, void* stream);
 
-/* Kernel-path override for tests and tuning (no reference counterpart).
- * key "force_path": 0 = automatic, 1 = skinny split-K MFMA, 2 = tiled MFMA,
- * 3 = generic.  key "skinny_wg_per_cu": workgroups per CU the split-K planner
- * aims for (default 4).  Returns MQ_INVALID_ARGUMENT for an unknown key. */
+/* Kernel-path override and layout knobs for tests and tuning (no reference
+ * counterpart).  Keys: "force_path" (0 automatic, 2 tiled MFMA GEMM,
+ * 3 generic, 6 decode GEMV), "decode_rpw" (weight rows per MFMA tile:
+ * 0 automatic, 1..16), "decode_max_nw" (wavefronts per workgroup: 4, 8, 16),
+ * "decode_wg_per_cu" (1..8), "decode_min_chunks" (stage K in at least this
+ * many chunks: 0..64).  Returns MQ_INVALID_ARGUMENT for an unknown key or value. */
 MQ_API int mq_set_option(const char* key, int64_t value);
 
 /* Kernel the last successful mq_dequant_matmul / mq_vecmat_f16 call on this
- * thread launched: 1 skinny, 2 tiled, 3 generic, 4 vecmat [K,N]. */
+ * thread launched: 2 tiled, 3 generic, 4 vecmat [K,N], 6 decode. */
 MQ_API int mq_last_path(void);
 
 MQ_API const char* mq_last_error(void);

@@ -1,6 +1,6 @@
 // C-ABI entry points: argument validation (mirroring src/ops/matmul.mm:910-934),
-// kernel-path selection and launch.  No allocation happens here: outputs and
-// workspace are the caller's.
+// kernel-path selection and launch.  No allocation happens here: the caller
+// owns every buffer, and no kernel needs memory beyond inputs and outputs.
 #include <hip/hip_runtime.h>
 
 #include <atomic>
@@ -16,11 +16,10 @@ namespace {
 thread_local std::string g_last_error;
 thread_local int g_last_path = 0;
 std::atomic<int> g_force_path{0};
-std::atomic<int> g_wg_per_cu{4};
-std::atomic<int> g_splitk_nofence{0};
-std::atomic<int> g_gemv_max_nw{16};
-std::atomic<int> g_gemv_xfull{1};
-std::atomic<int> g_gemv_rpw{0};
+std::atomic<int> g_dec_rpw{0};
+std::atomic<int> g_dec_nw{16};
+std::atomic<int> g_dec_wpc{1};
+std::atomic<int> g_dec_chunks{0};
 
 int fail(int code, const std::string& msg) {
   g_last_error = msg;
@@ -45,55 +44,48 @@ int num_cus_current() {
   return cache[dev];
 }
 
-enum Path {
-  PATH_AUTO = 0, PATH_SPLITK = 1, PATH_TILED = 2, PATH_GENERIC = 3, PATH_VECMAT_KN = 4, PATH_GEMV = 5
-};
+// Path ids (mq_last_path / force_path); 1 and 5 are retired ids of earlier
+// decode kernels and are not reused.
+enum Path { PATH_AUTO = 0, PATH_TILED = 2, PATH_GENERIC = 3, PATH_VECMAT_KN = 4, PATH_DECODE = 6 };
+
+mq::DecodeTuning decode_tuning() {
+  mq::DecodeTuning t;
+  t.rpw = g_dec_rpw.load();
+  t.max_nw = g_dec_nw.load();
+  t.wg_per_cu = g_dec_wpc.load();
+  t.force_chunks = g_dec_chunks.load();
+  return t;
+}
+
+bool decode_ok(const mq::LinearArgs& a) {
+  return mq::decode_supported(a) && mq::decode_plan(a, num_cus_current(), decode_tuning()).ok;
+}
 
 int choose_path(const mq::LinearArgs& a) {
   int forced = g_force_path.load();
-  if (forced == PATH_SPLITK && mq::skinny_supported(a)) return PATH_SPLITK;
-  if (forced == PATH_GEMV && mq::gemv_supported(a)) return PATH_GEMV;
+  if (forced == PATH_DECODE && decode_ok(a)) return PATH_DECODE;
   if (forced == PATH_TILED && mq::tiled_supported(a)) return PATH_TILED;
   if (forced == PATH_GENERIC) return PATH_GENERIC;
-  if (a.M <= 64 && mq::gemv_supported(a)) return PATH_GEMV;
+  if (decode_ok(a)) return PATH_DECODE;
   if (mq::tiled_supported(a)) return PATH_TILED;
   return PATH_GENERIC;
 }
 
-mq::SkinnyPlan plan_for(const mq::LinearArgs& a) {
-  mq::SkinnyPlan p = mq::skinny_plan(a, num_cus_current() * g_wg_per_cu.load() / 4, 0);
-  p.nofence = g_splitk_nofence.load();
-  return p;
-}
-
-int run_linear(const mq::LinearArgs& a, void* ws, size_t ws_bytes, hipStream_t s) {
-  int path = choose_path(a);
+int run_linear(const mq::LinearArgs& a, hipStream_t s) {
+  const int path = choose_path(a);
   hipError_t e;
-  if (path == PATH_GEMV) {
-    mq::GemvTuning t;
-    t.allow_full = g_gemv_xfull.load() != 0;
-    t.max_nw = g_gemv_max_nw.load();
-    t.rpw = g_gemv_rpw.load();
-    e = mq::gemv_launch(a, mq::gemv_plan(a, t), s);
-  } else if (path == PATH_SPLITK) {
-    mq::SkinnyPlan p = plan_for(a);
-    if (p.ws_bytes > 0 && (ws == nullptr || ws_bytes < p.ws_bytes))
-      return fail(MQ_INVALID_ARGUMENT, "dequant_matmul: workspace too small (need " +
-                                           std::to_string(p.ws_bytes) + " bytes)");
-    if (p.ws_bytes > 0 && ((uintptr_t)ws & 255))
-      return fail(MQ_INVALID_ARGUMENT, "dequant_matmul: workspace must be 256-byte aligned");
-    e = mq::skinny_launch(a, p, ws, s);
-  } else if (path == PATH_TILED) {
+  if (path == PATH_DECODE)
+    e = mq::decode_launch(a, mq::decode_plan(a, num_cus_current(), decode_tuning()), s);
+  else if (path == PATH_TILED)
     e = mq::tiled_launch(a, s);
-  } else {
+  else
     e = mq::generic_linear_launch(a, s);
-  }
   if (e != hipSuccess) return hip_fail(e, "dequant_matmul: kernel launch failed");
   g_last_path = path;
   return MQ_SUCCESS;
 }
 
-// Shared validation of mq_dequant_matmul / the workspace query.
+// Validation shared by the linear entry points.
 int build_args(mq::LinearArgs& a, int64_t M, int64_t N, int64_t K, int32_t group_size,
                int32_t quant_type, int32_t epilogue) {
   if (M < 1 || N < 1 || K < 1)
@@ -128,8 +120,7 @@ extern "C" {
 MQ_API int mq_dequant_matmul(const void* activations, int64_t lda, const void* weights_packed,
                              int64_t ldw_bytes, const void* scales, const void* zeros, void* out,
                              int64_t ldc, int64_t M, int64_t N, int64_t K, int32_t group_size,
-                             int32_t quant_type, int32_t epilogue, const void* bias, void* workspace,
-                             size_t workspace_bytes, void* stream) {
+                             int32_t quant_type, int32_t epilogue, const void* bias, void* stream) {
   mq::LinearArgs a{};
   int rc = build_args(a, M, N, K, group_size, quant_type, epilogue);
   if (rc != MQ_SUCCESS) return rc;
@@ -149,19 +140,7 @@ MQ_API int mq_dequant_matmul(const void* activations, int64_t lda, const void* w
   a.W = weights_packed; a.ldw = ldw_bytes;
   a.scales = scales; a.zeros = zeros; a.bias = bias;
   a.C = out; a.ldc = ldc;
-  return run_linear(a, workspace, workspace_bytes, (hipStream_t)stream);
-}
-
-MQ_API size_t mq_dequant_matmul_workspace_size(int64_t M, int64_t N, int64_t K, int32_t group_size,
-                                               int32_t quant_type, int32_t epilogue) {
-  mq::LinearArgs a{};
-  if (build_args(a, M, N, K, group_size, quant_type, epilogue) != MQ_SUCCESS) return 0;
-  // alignment-independent shape checks only: assume aligned operands
-  a.lda = K; a.ldw = quant_type == MQ_QUANT_INT4 ? K / 2 : K; a.ldc = N;
-  a.A = (const void*)256; a.W = (const void*)256;
-  if (a.ldw & 15) return 0;
-  if (choose_path(a) != PATH_SPLITK) return 0;
-  return plan_for(a).ws_bytes;
+  return run_linear(a, (hipStream_t)stream);
 }
 
 MQ_API int mq_dequantize(const void* weights_packed, int64_t ldw_bytes, const void* scales,
@@ -196,8 +175,7 @@ MQ_API int mq_dequantize(const void* weights_packed, int64_t ldw_bytes, const vo
 }
 
 MQ_API int mq_vecmat_f16(const void* a, int64_t lda, const void* b, int64_t ldb, void* c, int64_t ldc,
-                         int64_t M, int64_t N, int64_t K, int32_t transpose_b, void* workspace,
-                         size_t workspace_bytes, void* stream) {
+                         int64_t M, int64_t N, int64_t K, int32_t transpose_b, void* stream) {
   if (!a || !b || !c) return fail(MQ_INVALID_ARGUMENT, "matmul: null pointer argument");
   if (M < 1 || N < 1 || K < 1 || M > INT32_MAX || N > INT32_MAX || K > INT32_MAX)
     return fail(MQ_INVALID_ARGUMENT, "matmul: bad shape");
@@ -217,29 +195,11 @@ MQ_API int mq_vecmat_f16(const void* a, int64_t lda, const void* b, int64_t ldb,
   la.g = 1; la.G = 1;
   la.fmt = mq::FMT_F16;
   la.epi = mq::EPI_NONE;
-  int path = choose_path(la);
-  if (path == PATH_TILED) path = PATH_GENERIC;  // the tiled kernel takes quantized weights only
-  if (path == PATH_GEMV || path == PATH_SPLITK)
-    return run_linear(la, workspace, workspace_bytes, (hipStream_t)stream);
+  if (choose_path(la) == PATH_DECODE) return run_linear(la, (hipStream_t)stream);
   hipError_t e = mq::generic_linear_launch(la, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "matmul: kernel launch failed");
   g_last_path = PATH_GENERIC;
   return MQ_SUCCESS;
-}
-
-MQ_API size_t mq_vecmat_f16_workspace_size(int64_t M, int64_t N, int64_t K, int32_t transpose_b) {
-  if (!transpose_b || M < 1 || N < 1 || K < 1) return 0;
-  mq::LinearArgs la{};
-  la.A = (const void*)256; la.lda = K;
-  la.W = (const void*)256; la.ldw = K * 2;
-  la.ldc = N;
-  la.M = (int)M; la.N = (int)N; la.K = (int)K;
-  la.g = 1; la.G = 1;
-  la.fmt = mq::FMT_F16;
-  la.epi = mq::EPI_NONE;
-  if (la.ldw & 15) return 0;
-  if (choose_path(la) != PATH_SPLITK) return 0;
-  return plan_for(la).ws_bytes;
 }
 
 MQ_API int mq_swiglu_f16(const void* gate, const void* up, void* out, int64_t n, void* stream) {
@@ -254,34 +214,31 @@ MQ_API int mq_swiglu_f16(const void* gate, const void* up, void* out, int64_t n,
 MQ_API int mq_set_option(const char* key, int64_t value) {
   if (!key) return fail(MQ_INVALID_ARGUMENT, "set_option: null key");
   if (std::strcmp(key, "force_path") == 0) {
-    if (value < 0 || value > 5 || value == PATH_VECMAT_KN)
-      return fail(MQ_INVALID_ARGUMENT, "set_option: force_path must be 0, 1, 2, 3 or 5");
+    if (value != PATH_AUTO && value != PATH_TILED && value != PATH_GENERIC && value != PATH_DECODE)
+      return fail(MQ_INVALID_ARGUMENT, "set_option: force_path must be 0, 2, 3 or 6");
     g_force_path.store((int)value);
     return MQ_SUCCESS;
   }
-  if (std::strcmp(key, "skinny_wg_per_cu") == 0) {
-    if (value < 1 || value > 64) return fail(MQ_INVALID_ARGUMENT, "set_option: skinny_wg_per_cu must be 1..64");
-    g_wg_per_cu.store((int)value);
+  if (std::strcmp(key, "decode_rpw") == 0) {
+    if (value != 0 && value != 1 && value != 2 && value != 4 && value != 8 && value != 16)
+      return fail(MQ_INVALID_ARGUMENT, "set_option: decode_rpw must be 0, 1, 2, 4, 8 or 16");
+    g_dec_rpw.store((int)value);
     return MQ_SUCCESS;
   }
-  if (std::strcmp(key, "splitk_nofence") == 0) {  // timing experiments only: results are not valid
-    g_splitk_nofence.store(value ? 1 : 0);
+  if (std::strcmp(key, "decode_max_nw") == 0) {
+    if (value != 4 && value != 8 && value != 16)
+      return fail(MQ_INVALID_ARGUMENT, "set_option: decode_max_nw must be 4, 8 or 16");
+    g_dec_nw.store((int)value);
     return MQ_SUCCESS;
   }
-  if (std::strcmp(key, "gemv_xfull") == 0) {
-    g_gemv_xfull.store(value ? 1 : 0);
+  if (std::strcmp(key, "decode_wg_per_cu") == 0) {
+    if (value < 1 || value > 8) return fail(MQ_INVALID_ARGUMENT, "set_option: decode_wg_per_cu must be 1..8");
+    g_dec_wpc.store((int)value);
     return MQ_SUCCESS;
   }
-  if (std::strcmp(key, "gemv_rpw") == 0) {
-    if (value != 0 && value != 2 && value != 4 && value != 8 && value != 16)
-      return fail(MQ_INVALID_ARGUMENT, "set_option: gemv_rpw must be 0, 2, 4, 8 or 16");
-    g_gemv_rpw.store((int)value);
-    return MQ_SUCCESS;
-  }
-  if (std::strcmp(key, "gemv_max_nw") == 0) {
-    if (value != 2 && value != 4 && value != 8 && value != 16)
-      return fail(MQ_INVALID_ARGUMENT, "set_option: gemv_max_nw must be 2, 4, 8 or 16");
-    g_gemv_max_nw.store((int)value);
+  if (std::strcmp(key, "decode_min_chunks") == 0) {
+    if (value < 0 || value > 64) return fail(MQ_INVALID_ARGUMENT, "set_option: decode_min_chunks must be 0..64");
+    g_dec_chunks.store((int)value);
     return MQ_SUCCESS;
   }
   return fail(MQ_INVALID_ARGUMENT, std::string("set_option: unknown key ") + key);
@@ -306,6 +263,6 @@ MQ_API const char* mq_error_to_string(int code) {
   }
 }
 
-MQ_API int mq_abi_version(void) { return 1; }
+MQ_API int mq_abi_version(void) { return 2; }
 
 }  // extern "C"

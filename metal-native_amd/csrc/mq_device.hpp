@@ -140,6 +140,17 @@ __device__ __forceinline__ f4 mfma16x16x32(h8 a, h8 b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
+// Read-out fence for MFMA accumulators: 24 wait states with the accumulator
+// as an in/out operand, so the MFMA that wrote it has retired before any
+// VALU/LDS/VMEM instruction reads it.  The compiler pads a VALU read of a
+// v_mfma_f32_16x16x32_f16 result on gfx950 with about 8 wait states, and
+// reads placed that close were measured to see stale upper accumulator
+// registers; every read-out of an MFMA result in this library goes through
+// this fence.
+__device__ __forceinline__ void mfma_result_fence(f4& v) {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+v"(v));
+}
+
 __device__ __forceinline__ float silu_f32(float v) { return v / (1.0f + expf(-v)); }
 
 // Scalar dequant of one element (generic kernels).

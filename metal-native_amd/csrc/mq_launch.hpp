@@ -10,12 +10,6 @@ namespace mq {
 enum Fmt { FMT_INT4 = 0, FMT_INT8 = 1, FMT_F16 = 2 };
 enum Epi { EPI_NONE = 0, EPI_BIAS = 1, EPI_SWIGLU = 2 };
 
-// Split-K workspace layout: a fixed-size counter region (zero between calls)
-// followed by the fp32 partial sums.  The counter region's size does not
-// depend on the problem, so partials of one call never overlap counters of
-// another call that shares the workspace.
-constexpr size_t kWsCounterBytes = 65536;
-
 // One quantized (or fp16) linear: C[M, Nout] = epi(A[M,K] . W[N,K]^T).
 struct LinearArgs {
   const void* A;        // fp16 [M, K], row stride lda (elements)
@@ -34,43 +28,23 @@ struct LinearArgs {
   int F;                // SwiGLU half width (N = 2F), 0 otherwise
 };
 
-// Split-K launch geometry chosen on the host for the skinny kernel.
-struct SkinnyPlan {
-  int steps;      // 16-byte loads per lane per K chunk
-  int mblocks;    // 16-row blocks of A (M <= 16*mblocks)
-  int splits;     // number of K chunks (grid.y)
-  int kchunk;     // K elements per chunk
-  int rblocks;    // weight-row blocks (grid.x)
+// Persistent row-range GEMV (decode, M <= 16).
+struct DecodeTuning {
+  int rpw = 0;           // weight rows per MFMA tile (0 = from M and K)
+  int max_nw = 16;       // wavefronts per workgroup
+  int wg_per_cu = 1;     // workgroups per CU the rows are spread over
+  int force_chunks = 0;  // tests: stage K in at least this many chunks
+};
+struct DecodePlan {
+  int rpw, nw, rows_wg, nwg, nsteps, spc, nchunks, xs_stride, xp;
+  uint32_t off_szs, off_red, off_bnd, off_ws;
+  int sz_chunks;
   size_t lds_bytes;
-  size_t ws_bytes;  // workspace needed (counters + partials); 0 if splits == 1
-  int nofence;      // timing experiments only
+  bool ok;
 };
-
-bool skinny_supported(const LinearArgs& a);
-SkinnyPlan skinny_plan(const LinearArgs& a, int num_cus, size_t ws_avail);
-hipError_t skinny_launch(const LinearArgs& a, const SkinnyPlan& p, void* ws, hipStream_t s);
-
-// Row-block GEMV (no split-K workspace).
-struct GemvTuning {
-  bool allow_full = true;  // whole-K activations in LDS when they fit
-  int max_nw = 16;         // cap on wavefronts per workgroup
-  int rpw = 0;             // weight rows per unit (0 = by M)
-};
-struct GemvPlan {
-  int nw;         // wavefronts per workgroup (K split inside the workgroup)
-  int rpw;        // weight rows per unit (whole-K kernel)
-  int xs_stride;  // LDS activation row stride in halves (whole-K kernel)
-  int mblocks;    // 16-row blocks of A
-  int rowblocks;  // workgroups (16 weight rows each)
-  int nchunks;    // K chunks (one step per wave each)
-  int nsteps;     // K steps of 4 16-byte pieces per row
-  int kpad;       // K rounded up to whole steps
-  bool xfull;     // whole activation matrix staged in LDS
-  size_t lds_bytes;
-};
-bool gemv_supported(const LinearArgs& a);
-GemvPlan gemv_plan(const LinearArgs& a, const GemvTuning& t);
-hipError_t gemv_launch(const LinearArgs& a, const GemvPlan& p, hipStream_t s);
+bool decode_supported(const LinearArgs& a);
+DecodePlan decode_plan(const LinearArgs& a, int num_cus, const DecodeTuning& t);
+hipError_t decode_launch(const LinearArgs& a, const DecodePlan& p, hipStream_t s);
 
 bool tiled_supported(const LinearArgs& a);
 hipError_t tiled_launch(const LinearArgs& a, hipStream_t s);

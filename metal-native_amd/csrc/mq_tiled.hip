@@ -145,6 +145,10 @@ __global__ __launch_bounds__(kThreads, 2) void tiled_kernel(TiledKArgs p) {
   }
 
   // ---- epilogue ----
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) mfma_result_fence(acc[i][j]);
   // Lane holds D[row = 16*i + 4*(lane>>4) + r][col = 16*j + (lane&15)] of the wave sub-tile.
   if (EPI == EPI_SWIGLU) {
     // up waves (wn == 1) hand half(up) to the gate waves through LDS

@@ -27,24 +27,20 @@ EPILOGUE_NONE = 0
 EPILOGUE_BIAS = 1
 EPILOGUE_SWIGLU = 2
 
-PATH_NAMES = {0: "none", 1: "splitk", 2: "tiled", 3: "generic", 4: "vecmat_kn", 5: "gemv"}
+PATH_NAMES = {0: "none", 2: "tiled", 3: "generic", 4: "vecmat_kn", 6: "decode"}
 
 _c_void_p = ctypes.c_void_p
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int32
-_size = ctypes.c_size_t
 
 # name -> (restype, argtypes)
 SIGNATURES = {
     "mq_dequant_matmul": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p,
-                                 _i64, _i64, _i64, _i64, _i32, _i32, _i32, _c_void_p, _c_void_p,
-                                 _size, _c_void_p]),
-    "mq_dequant_matmul_workspace_size": (_size, [_i64, _i64, _i64, _i32, _i32, _i32]),
+                                 _i64, _i64, _i64, _i64, _i32, _i32, _i32, _c_void_p, _c_void_p]),
     "mq_dequantize": (_i32, [_c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64,
                              _i32, _i32, _i32, _c_void_p]),
     "mq_vecmat_f16": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _i64, _i64, _i64, _i64,
-                             _i32, _c_void_p, _size, _c_void_p]),
-    "mq_vecmat_f16_workspace_size": (_size, [_i64, _i64, _i64, _i32]),
+                             _i32, _c_void_p]),
     "mq_swiglu_f16": (_i32, [_c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p]),
     "mq_set_option": (_i32, [ctypes.c_char_p, _i64]),
     "mq_last_path": (_i32, []),

@@ -20,7 +20,6 @@ buffers.  Outputs are fresh tensors owned by the caller.
 from __future__ import annotations
 
 import ctypes
-import threading
 
 import torch
 
@@ -57,33 +56,6 @@ def _stream_handle(device: torch.device) -> int:
 
 def _ptr(t: torch.Tensor | None):
     return None if t is None else ctypes.c_void_p(t.data_ptr())
-
-
-# ---------------------------------------------------------------------------
-# split-K workspace: one zero-initialised buffer per (device, stream), grown on
-# demand.  The kernels leave its counter region zero after every call, so a
-# buffer is reusable by every later call ordered on the same stream.
-# ---------------------------------------------------------------------------
-_ws_lock = threading.Lock()
-_ws_cache: dict[tuple[int, int], torch.Tensor] = {}
-
-
-def _workspace(device: torch.device, nbytes: int) -> tuple[torch.Tensor | None, int]:
-    if nbytes == 0:
-        return None, 0
-    key = (device.index, _stream_handle(device))
-    with _ws_lock:
-        buf = _ws_cache.get(key)
-        if buf is None or buf.numel() < nbytes:
-            if torch.cuda.is_current_stream_capturing():
-                _invalid("dequant_matmul: split-K workspace must be allocated before graph capture "
-                         "(run the op once eagerly on this stream first)")
-            # round up so that nearby shapes share one buffer
-            size = max(nbytes, 1 << 20)
-            size = 1 << (size - 1).bit_length()
-            buf = torch.zeros(size, dtype=torch.uint8, device=device)
-            _ws_cache[key] = buf
-    return buf, buf.numel()
 
 
 def _require_cuda(t: torch.Tensor, what: str, op: str):
@@ -190,11 +162,9 @@ def dequant_matmul(activations: torch.Tensor, weights_packed: torch.Tensor, scal
     if M == 0 or n_out == 0:
         return out
     with torch.cuda.device(dev):
-        need = _L.mq_dequant_matmul_workspace_size(M, N, K, group_size, qt, epi)
-        ws, ws_bytes = _workspace(dev, need)
         rc = _L.mq_dequant_matmul(
             _ptr(activations), lda, _ptr(weights_packed), ldw, _ptr(scales), _ptr(zeros), _ptr(out),
-            n_out, M, N, K, group_size, qt, epi, _ptr(bias), _ptr(ws), ws_bytes, _stream_handle(dev))
+            n_out, M, N, K, group_size, qt, epi, _ptr(bias), _stream_handle(dev))
     _check(rc)
     return out
 
@@ -365,11 +335,9 @@ def matmul(a: torch.Tensor, b: torch.Tensor, transpose_a: bool = False,
         for r0 in range(0, rows, 64):
             r1 = min(rows, r0 + 64)
             ai = a2[r0:r1]
-            need = _L.mq_vecmat_f16_workspace_size(r1 - r0, N, K, 1 if transpose_b else 0)
-            ws, ws_bytes = _workspace(dev, need)
             rc = _L.mq_vecmat_f16(_ptr(ai), _rows(ai, "a", op), _ptr(b), _rows(b, "b", op),
                                   _ptr(out[r0:r1]), N, r1 - r0, N, K, 1 if transpose_b else 0,
-                                  _ptr(ws), ws_bytes, _stream_handle(dev))
+                                  _stream_handle(dev))
             _check(rc)
     return out.reshape(*lead, M, N)
 

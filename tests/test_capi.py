@@ -26,8 +26,7 @@ def lib():
 
 def test_header_declares_entry_points():
     names = declared()
-    for want in ["mq_dequant_matmul", "mq_dequant_matmul_workspace_size", "mq_dequantize",
-                 "mq_vecmat_f16", "mq_vecmat_f16_workspace_size", "mq_swiglu_f16", "mq_last_error"]:
+    for want in ["mq_dequant_matmul", "mq_dequantize", "mq_vecmat_f16", "mq_swiglu_f16", "mq_last_error"]:
         assert want in names
 
 
@@ -40,7 +39,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version_and_error_strings(lib):
-    assert lib.mq_abi_version() == 1
+    assert lib.mq_abi_version() == 2
     assert lib.mq_error_to_string(0) == b"Success"
     assert lib.mq_error_to_string(4) == b"InvalidArgument"
     assert lib.mq_error_to_string(8) == b"NotImplemented"
@@ -50,7 +49,7 @@ def test_validation_without_gpu(lib):
     P = ctypes.c_void_p(256)  # never dereferenced: validation fails first
     call = lambda M, N, K, g, qt, epi, ldw=None: lib.mq_dequant_matmul(
         P, K, P, (K // 2 if qt == 0 else K) if ldw is None else ldw, P, P, P, N, M, N, K, g, qt, epi,
-        None, None, 0, None)
+        None, None)
     assert call(0, 8, 32, 32, 0, 0) == 4
     assert b"positive" in lib.mq_last_error()
     assert call(1, 8, 33, 32, 0, 0) == 4  # odd K for int4
@@ -65,11 +64,14 @@ def test_validation_without_gpu(lib):
     assert b"bias" in lib.mq_last_error()
     assert lib.mq_dequantize(P, 16, P, P, P, 32, 4, 32, 32, 0, 1, None) == 4  # flat + zeros
     assert lib.mq_swiglu_f16(None, P, P, 10, None) == 4
-    assert lib.mq_vecmat_f16(P, 10, P, 10, P, 10, 1, 300, 300, 1, None, 0, None) == 4  # lda < K
+    assert lib.mq_vecmat_f16(P, 10, P, 10, P, 10, 1, 300, 300, 1, None) == 4  # lda < K
 
 
 def test_set_option(lib):
     assert lib.mq_set_option(b"force_path", 9) == 4
+    assert lib.mq_set_option(b"force_path", 1) == 4  # retired path id
+    assert lib.mq_set_option(b"decode_rpw", 3) == 4
+    assert lib.mq_set_option(b"decode_max_nw", 2) == 4
     assert lib.mq_set_option(b"nonsense", 1) == 4
     assert b"unknown key" in lib.mq_last_error()
     assert lib.mq_set_option(b"force_path", 0) == 0

@@ -6,7 +6,7 @@ Bars (from the task's contract):
   fp32-accumulated result (TOL_ABS / TOL_REL below), every row of A;
 * SwiGLU: the same bound against the oracle's fp16 composition (exp differs
   by ulps between implementations).
-Every kernel path (skinny split-K MFMA, tiled MFMA, generic) is forced in turn
+Every kernel path (decode GEMV, tiled MFMA GEMM, generic) is forced in turn
 on the reference's known-answer cases and on seeded random problems.
 """
 
@@ -25,7 +25,7 @@ TOL_ABS = 1e-2
 TOL_REL = 1e-3
 GOLD = os.path.join(os.path.dirname(__file__), "golden", "known_answers.npz")
 
-PATHS = {"splitk": 1, "tiled": 2, "generic": 3, "gemv": 5}
+PATHS = {"tiled": 2, "generic": 3, "decode": 6}
 
 
 @pytest.fixture(scope="module")
@@ -108,7 +108,7 @@ def golden_cases():
     return g, sorted({k.split("/")[0] for k in g.files})
 
 
-@pytest.mark.parametrize("path", [None, "gemv", "splitk", "tiled", "generic"])
+@pytest.mark.parametrize("path", [None, "decode", "tiled", "generic"])
 def test_known_answers(mn, gpu, path):
     gold, names = golden_cases()
     h = lambda k: gold[k].view(np.float16)
@@ -139,18 +139,18 @@ SMALL = [
 ]
 
 
-@pytest.mark.parametrize("path", [None, "gemv", "splitk", "tiled"])
+@pytest.mark.parametrize("path", [None, "decode", "tiled"])
 @pytest.mark.parametrize("M,K,N,g", SMALL)
 def test_int4_random(mn, gpu, path, M, K, N, g):
     say(f"int4 M={M} K={K} N={N} g={g} path={path}")
     x, wp, s, z = O.make_int4_problem(M, K, N, g, seed=M * 7 + K + N)
     ref = O.matmul_f32acc(x, O.dequant_int4(wp, s, z, K, g))
     y, taken = run_dm(mn, gpu, x, wp, s, z, g, "int4", path)
-    expect_path(path, taken, shape_ok=not (path in ("gemv", "splitk") and M > 64))
+    expect_path(path, taken, shape_ok=not (path == "decode" and M > 16))
     check_close(y, ref, f"int4 {M}x{K}x{N} g{g} [{taken}]")
 
 
-@pytest.mark.parametrize("path", [None, "gemv", "splitk", "tiled"])
+@pytest.mark.parametrize("path", [None, "decode", "tiled"])
 @pytest.mark.parametrize("M,K,N", [(1, 256, 64), (4, 512, 96), (16, 1024, 128), (64, 512, 192),
                                    (100, 256, 160)])
 def test_int8_random(mn, gpu, path, M, K, N):
@@ -159,7 +159,7 @@ def test_int8_random(mn, gpu, path, M, K, N):
     zz = (np.random.default_rng(1).uniform(-0.01, 0.01, s.shape)).astype(np.float16)  # exercise zeros
     ref = O.matmul_f32acc(x, O.dequant_int8(q, s, zz, K, g))
     y, taken = run_dm(mn, gpu, x, q, s, zz, g, "int8", path)
-    expect_path(path, taken, shape_ok=not (path in ("gemv", "splitk") and M > 64))
+    expect_path(path, taken, shape_ok=not (path == "decode" and M > 16))
     check_close(y, ref, f"int8 {M}x{K}x{N} [{taken}]")
 
 
@@ -173,7 +173,7 @@ def test_unaligned_shapes(mn, gpu, M, K, N):
     check_close(y, ref, f"unaligned int4 {M}x{K}x{N} [{taken}]")
 
 
-@pytest.mark.parametrize("path", [None, "gemv", "splitk", "tiled", "generic"])
+@pytest.mark.parametrize("path", [None, "decode", "tiled", "generic"])
 @pytest.mark.parametrize("M", [1, 5, 64, 130])
 def test_epilogues(mn, gpu, path, M):
     say(f"epilogues M={M} path={path}")
@@ -197,7 +197,7 @@ def test_config2_qwen7b_down(mn, gpu, M):
     K, N, g = 18944, 3584, 128
     x, wp, s, z = O.make_int4_problem(M, K, N, g, seed=0)
     ref = O.matmul_f32acc(x, O.dequant_int4(wp, s, z, K, g))
-    for path in ("gemv", "splitk"):
+    for path in ("decode", "tiled"):
         y, taken = run_dm(mn, gpu, x, wp, s, z, g, "int4", path)
         assert taken == path
         check_close(y, ref, f"config2 M={M} [{path}]")
@@ -227,7 +227,7 @@ def test_config4_int8_swiglu(mn, gpu, M):
     K, F = 3584, 18944
     x, q, s, z, g = O.make_int8_problem(M, K, 2 * F, seed=0)
     acc = O.matmul_f32acc(x, O.dequant_int8(q, s, z, K, g))
-    for path in ("gemv", "splitk"):
+    for path in (("decode", "tiled") if M <= 16 else ("tiled",)):
         y, taken = run_dm(mn, gpu, x, q, s, z, g, "int8", path, epilogue="swiglu")
         assert y.shape == (M, F) and taken == path
         check_swiglu(y, acc, f"config4 M={M} [{path}]")
@@ -315,12 +315,12 @@ def test_vecmat_route(mn, gpu, M, K, N, transpose_b):
     b = (rng.standard_normal((N, K) if transpose_b else (K, N)) * 0.05).astype(np.float16)
     got = host(mn.matmul(dev(a, gpu), dev(b, gpu), False, transpose_b))
     ref = a.astype(np.float32) @ (b.T if transpose_b else b).astype(np.float32)
-    assert mn.last_path() in ("gemv", "vecmat_kn", "generic")
+    assert mn.last_path() in ("decode", "vecmat_kn", "generic")
     check_close(got, ref, f"vecmat tb={transpose_b}")
 
 
 # ---------------------------------------------------------------------------
-# behaviour: determinism, row independence, workspace reuse, graphs, errors
+# behaviour: determinism, row independence, repeated calls, graphs, errors
 # ---------------------------------------------------------------------------
 
 def test_split_k_is_deterministic(mn, gpu):
@@ -345,8 +345,8 @@ def test_rows_are_independent(mn, gpu):
     assert np.abs(y8[1:] - y8[:1]).max() > 0
 
 
-def test_workspace_reuse_across_shapes(mn, gpu):
-    say("workspace reuse")
+def test_repeated_calls_across_shapes(mn, gpu):
+    say("repeated calls across shapes")
     probs = [O.make_int4_problem(M, K, N, 128, seed=M + K) for M, K, N in
              [(1, 8192, 1024), (8, 4096, 2048), (3, 16384, 512), (1, 8192, 1024)]]
     refs = [O.matmul_f32acc(x, O.dequant_int4(wp, s, z, x.shape[1], 128)) for x, wp, s, z in probs]
@@ -357,8 +357,8 @@ def test_workspace_reuse_across_shapes(mn, gpu):
 
 
 def test_hip_graph_replay(mn, gpu):
-    """Capture the decode GEMV (split-K with its counters) in a HIP graph and
-    replay it several times with eager work in between."""
+    """Capture the decode GEMV in a HIP graph and replay it several times with
+    eager work in between."""
     say("graph replay")
     x, wp, s, z = O.make_int4_problem(4, 18944, 3584, 128, seed=3)
     xa, wa, sa, za = (dev(v, gpu) for v in (x, wp, s, z))
@@ -366,7 +366,7 @@ def test_hip_graph_replay(mn, gpu):
     stream = torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(stream):
-        mn.dequant_matmul(xa, wa, sa, za, 128, "int4")  # allocate this stream's workspace
+        mn.dequant_matmul(xa, wa, sa, za, 128, "int4")  # warm up on the capture stream
     torch.cuda.current_stream().wait_stream(stream)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
@@ -402,29 +402,48 @@ def test_errors_on_gpu_tensors(mn, gpu):
     assert mn.dequant_matmul(x, w8, s, s, 32, "whatever").shape == (2, 8)
 
 
-@pytest.mark.parametrize("rpw", [2, 4, 8, 16])
-@pytest.mark.parametrize("max_nw", [8, 16])
-@pytest.mark.parametrize("M,K,N,g,qt", [(1, 18944, 512, 128, "int4"), (3, 4096, 200, 64, "int4"),
-                                        (4, 896, 4864, 64, "int4"), (2, 3584, 256, 3584, "int8"),
-                                        (8, 2304, 96, 32, "int4"), (1, 1008, 70, 1008, "int8"),
-                                        (2, 18944, 3584, 128, "int4")])
-def test_gemv_variants(mn, gpu, rpw, max_nw, M, K, N, g, qt):
-    """Every whole-K GEMV layout (rows per workgroup x K shifts) and workgroup
-    width against the oracle, including a K that is not a multiple of the step
-    and a group size that forces the generic kernel."""
-    say(f"gemv variant rpw={rpw} nw<={max_nw} M={M} K={K} N={N} g={g} {qt}")
+DECODE_SHAPES = [
+    # M, K, N, g, qt, epilogue
+    (1, 18944, 3584, 128, "int4", None), (3, 18944, 520, 128, "int4", None), (8, 18944, 600, 128, "int4", None),
+    (16, 4096, 300, 64, "int4", None), (2, 896, 4864, 64, "int4", "bias"), (5, 3584, 1000, 3584, "int8", "swiglu"),
+    (1, 3584, 2 * 700, 3584, "int8", "swiglu"), (12, 2048, 130, 32, "int4", "swiglu"), (7, 1008, 70, 1008, "int8", None),
+    (1, 32, 5, 32, "int4", None), (16, 640, 33, 128, "int8", "bias"),
+]
+
+
+@pytest.mark.parametrize("opts", [{}, {"decode_rpw": 16}, {"decode_max_nw": 4}, {"decode_wg_per_cu": 3},
+                                  {"decode_min_chunks": 3}, {"decode_min_chunks": 7, "decode_max_nw": 8}])
+@pytest.mark.parametrize("M,K,N,g,qt,epi", DECODE_SHAPES)
+def test_decode_variants(mn, gpu, opts, M, K, N, g, qt, epi):
+    """The persistent decode GEMV under every layout knob: rows per MFMA
+    tile, wavefronts per workgroup, workgroups per CU (tiles shared by
+    several waves) and K staged in several chunks, against the oracle."""
+    say(f"decode {opts} M={M} K={K} N={N} g={g} {qt} {epi}")
     if qt == "int4":
-        x, wp, s, z = O.make_int4_problem(M, K, N, g, seed=K + N)
-        ref = O.matmul_f32acc(x, O.dequant_int4(wp, s, z, K, g))
+        x, wp, s, z = O.make_int4_problem(M, K, N, g, seed=K + N + M)
+        acc = O.matmul_f32acc(x, O.dequant_int4(wp, s, z, K, g))
     else:
-        x, wp, s, z, g = O.make_int8_problem(M, K, N, seed=K + N, g=g)
-        ref = O.matmul_f32acc(x, O.dequant_int8(wp, s, z, K, g))
-    mn.set_option("gemv_rpw", rpw)
-    mn.set_option("gemv_max_nw", max_nw)
+        x, wp, s, z, g = O.make_int8_problem(M, K, N, seed=K + N + M, g=g)
+        z = np.random.default_rng(K).uniform(-0.01, 0.01, s.shape).astype(np.float16)
+        acc = O.matmul_f32acc(x, O.dequant_int8(wp, s, z, K, g))
+    kw = {}
+    b = None
+    if epi == "bias":
+        b = np.random.default_rng(N).standard_normal(N).astype(np.float16)
+        kw = {"epilogue": "bias", "bias": dev(b, gpu)}
+    elif epi == "swiglu":
+        kw = {"epilogue": "swiglu"}
+    for k, v in opts.items():
+        mn.set_option(k, v)
     try:
-        y, taken = run_dm(mn, gpu, x, wp, s, z, g, qt)
+        y, taken = run_dm(mn, gpu, x, wp, s, z, g, qt, "decode", **kw)
     finally:
-        mn.set_option("gemv_rpw", 0)
-        mn.set_option("gemv_max_nw", 16)
-    assert taken == "gemv"
-    check_close(y, ref, f"gemv rpw={rpw} [{taken}]")
+        for k, v in {"decode_rpw": 0, "decode_max_nw": 16, "decode_wg_per_cu": 1, "decode_min_chunks": 0}.items():
+            mn.set_option(k, v)
+    assert taken == "decode"
+    if epi == "swiglu":
+        check_swiglu(y, acc, f"decode {opts}")
+    elif epi == "bias":
+        check_close(y, acc + b.astype(np.float32), f"decode bias {opts}")
+    else:
+        check_close(y, acc, f"decode {opts}")
