@@ -60,7 +60,10 @@ enum mq_epilogue { MQ_EPILOGUE_NONE = 0, MQ_EPILOGUE_BIAS = 1, MQ_EPILOGUE_SWIGL
  * bindings/bind_ops.cpp:366-382).  Strides are in elements for A/out and in
  * bytes for the weights (ldw_bytes; K/2 for packed int4 rows, K for int8).
  * zeros may be NULL (no zero term); bias is read only for MQ_EPILOGUE_BIAS.
- * The kernels use no memory beyond the arguments. */
+ * The decode GEMV (M <= 16) splits K across workgroups; its partial sums and
+ * counters live in a library workspace kept per (device, stream), allocated
+ * by the first call on that stream that needs it (so that call must not be
+ * inside stream capture).  Calls on one stream are ordered and share it. */
 MQ_API int mq_dequant_matmul(const void* activations, int64_t lda, const void* weights_packed,
                              int64_t ldw_bytes, const void* scales, const void* zeros, void* out,
                              int64_t ldc, int64_t M, int64_t N, int64_t K, int32_t group_size,
@@ -92,10 +95,11 @@ MQ_API int mq_swiglu_f16(const void* gate, const void* up, void* out, int64_t n,
 
 /* Kernel-path override and layout knobs for tests and tuning (no reference
  * counterpart).  Keys: "force_path" (0 automatic, 2 tiled MFMA GEMM,
- * 3 generic, 6 decode GEMV), "decode_rpw" (weight rows per MFMA tile:
- * 0 automatic, 1..16), "decode_max_nw" (wavefronts per workgroup: 4, 8, 16),
- * "decode_wg_per_cu" (1..8), "decode_min_chunks" (stage K in at least this
- * many chunks: 0..64).  Returns MQ_INVALID_ARGUMENT for an unknown key or value. */
+ * 3 generic, 6 decode GEMV), "gemv_steps" (K steps per wavefront of the
+ * decode GEMV, 1..8, 0 automatic), "gemv_tiles_per_wg" (row tiles per
+ * workgroup: 1, 2 or 4, 0 automatic).  A layout the decode GEMV cannot stage
+ * makes it unavailable (the call then takes the tiled or generic kernel).
+ * Returns MQ_INVALID_ARGUMENT for an unknown key or value. */
 MQ_API int mq_set_option(const char* key, int64_t value);
 
 /* Kernel the last successful mq_dequant_matmul / mq_vecmat_f16 call on this

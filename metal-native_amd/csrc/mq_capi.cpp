@@ -1,12 +1,16 @@
 // C-ABI entry points: argument validation (mirroring src/ops/matmul.mm:910-934),
-// kernel-path selection and launch.  No allocation happens here: the caller
-// owns every buffer, and no kernel needs memory beyond inputs and outputs.
+// kernel-path selection and launch.  The caller owns inputs and outputs; the
+// split-K GEMV's partial sums and counters live in a library workspace, one
+// per (device, stream), allocated and zeroed on first use and grown on demand.
 #include <hip/hip_runtime.h>
 
 #include <atomic>
 #include <cstdio>
 #include <cstring>
+#include <map>
+#include <mutex>
 #include <string>
+#include <utility>
 
 #include "../../include/metal_native_amd.h"
 #include "mq_launch.hpp"
@@ -16,10 +20,8 @@ namespace {
 thread_local std::string g_last_error;
 thread_local int g_last_path = 0;
 std::atomic<int> g_force_path{0};
-std::atomic<int> g_dec_rpw{0};
-std::atomic<int> g_dec_nw{16};
-std::atomic<int> g_dec_wpc{1};
-std::atomic<int> g_dec_chunks{0};
+std::atomic<int> g_gemv_steps{0};
+std::atomic<int> g_gemv_tpw{0};
 
 int fail(int code, const std::string& msg) {
   g_last_error = msg;
@@ -46,26 +48,70 @@ int num_cus_current() {
 
 // Path ids (mq_last_path / force_path); 1 and 5 are retired ids of earlier
 // decode kernels and are not reused.
-enum Path { PATH_AUTO = 0, PATH_TILED = 2, PATH_GENERIC = 3, PATH_VECMAT_KN = 4, PATH_DECODE = 6 };
+enum Path { PATH_AUTO = 0, PATH_TILED = 2, PATH_GENERIC = 3, PATH_VECMAT_KN = 4, PATH_DECODE = 6, PATH_ROWS = 7 };
 
-mq::DecodeTuning decode_tuning() {
-  mq::DecodeTuning t;
-  t.rpw = g_dec_rpw.load();
-  t.max_nw = g_dec_nw.load();
-  t.wg_per_cu = g_dec_wpc.load();
-  t.force_chunks = g_dec_chunks.load();
+mq::GemvTuning gemv_tuning() {
+  mq::GemvTuning t;
+  t.steps = g_gemv_steps.load();
+  t.tpw = g_gemv_tpw.load();
   return t;
 }
 
 bool decode_ok(const mq::LinearArgs& a) {
-  return mq::decode_supported(a) && mq::decode_plan(a, num_cus_current(), decode_tuning()).ok;
+  return mq::gemv_supported(a) && mq::gemv_plan(a, num_cus_current(), gemv_tuning()).ok;
 }
+
+// Split-K workspace, one per (device, stream): counters must start at zero and
+// every launch leaves them at zero, so one hipMemset at allocation suffices.
+// Calls on one stream are ordered, so they may share it.
+struct Workspace {
+  void* ptr = nullptr;
+  size_t bytes = 0;
+};
+std::mutex g_ws_mu;
+std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
+
+hipError_t workspace_for(hipStream_t s, size_t need, void** out) {
+  *out = nullptr;
+  if (need == 0) return hipSuccess;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  std::lock_guard<std::mutex> lk(g_ws_mu);
+  Workspace& w = g_ws[{dev, s}];
+  if (w.bytes < need) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+      return hipErrorStreamCaptureUnsupported;  // first call on this stream must be outside capture
+    size_t nb = need < ((size_t)1 << 20) ? ((size_t)1 << 20) : need;
+    if (w.ptr) {
+      e = hipStreamSynchronize(s);  // the old buffer may still be in use on s
+      if (e != hipSuccess) return e;
+      (void)hipFree(w.ptr);
+      w.ptr = nullptr;
+      w.bytes = 0;
+    }
+    void* p = nullptr;
+    e = hipMalloc(&p, nb);
+    if (e != hipSuccess) return e;
+    e = hipMemset(p, 0, nb);
+    if (e != hipSuccess) { (void)hipFree(p); return e; }
+    w.ptr = p;
+    w.bytes = nb;
+  }
+  *out = w.ptr;
+  return hipSuccess;
+}
+
+bool rows_ok(const mq::LinearArgs& a) { return mq::rows_plan(a, num_cus_current()).ok; }
 
 int choose_path(const mq::LinearArgs& a) {
   int forced = g_force_path.load();
+  if (forced == PATH_ROWS && rows_ok(a)) return PATH_ROWS;
   if (forced == PATH_DECODE && decode_ok(a)) return PATH_DECODE;
   if (forced == PATH_TILED && mq::tiled_supported(a)) return PATH_TILED;
   if (forced == PATH_GENERIC) return PATH_GENERIC;
+  if (rows_ok(a)) return PATH_ROWS;
   if (decode_ok(a)) return PATH_DECODE;
   if (mq::tiled_supported(a)) return PATH_TILED;
   return PATH_GENERIC;
@@ -74,12 +120,22 @@ int choose_path(const mq::LinearArgs& a) {
 int run_linear(const mq::LinearArgs& a, hipStream_t s) {
   const int path = choose_path(a);
   hipError_t e;
-  if (path == PATH_DECODE)
-    e = mq::decode_launch(a, mq::decode_plan(a, num_cus_current(), decode_tuning()), s);
-  else if (path == PATH_TILED)
+  if (path == PATH_ROWS) {
+    e = mq::rows_launch(a, mq::rows_plan(a, num_cus_current()), s);
+  } else if (path == PATH_DECODE) {
+    const mq::GemvPlan pl = mq::gemv_plan(a, num_cus_current(), gemv_tuning());
+    void* ws = nullptr;
+    e = workspace_for(s, pl.ws_bytes, &ws);
+    if (e == hipErrorStreamCaptureUnsupported)
+      return fail(MQ_INVALID_ARGUMENT, "dequant_matmul: the split-K workspace of this stream is too small; "
+                                       "make one call of this shape on the stream before capturing it");
+    if (e != hipSuccess) return hip_fail(e, "dequant_matmul: workspace allocation failed");
+    e = mq::gemv_launch(a, pl, ws, s);
+  } else if (path == PATH_TILED) {
     e = mq::tiled_launch(a, s);
-  else
+  } else {
     e = mq::generic_linear_launch(a, s);
+  }
   if (e != hipSuccess) return hip_fail(e, "dequant_matmul: kernel launch failed");
   g_last_path = path;
   return MQ_SUCCESS;
@@ -195,7 +251,8 @@ MQ_API int mq_vecmat_f16(const void* a, int64_t lda, const void* b, int64_t ldb,
   la.g = 1; la.G = 1;
   la.fmt = mq::FMT_F16;
   la.epi = mq::EPI_NONE;
-  if (choose_path(la) == PATH_DECODE) return run_linear(la, (hipStream_t)stream);
+  const int pth = choose_path(la);
+  if (pth == PATH_DECODE || pth == PATH_ROWS) return run_linear(la, (hipStream_t)stream);
   hipError_t e = mq::generic_linear_launch(la, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "matmul: kernel launch failed");
   g_last_path = PATH_GENERIC;
@@ -214,31 +271,25 @@ MQ_API int mq_swiglu_f16(const void* gate, const void* up, void* out, int64_t n,
 MQ_API int mq_set_option(const char* key, int64_t value) {
   if (!key) return fail(MQ_INVALID_ARGUMENT, "set_option: null key");
   if (std::strcmp(key, "force_path") == 0) {
-    if (value != PATH_AUTO && value != PATH_TILED && value != PATH_GENERIC && value != PATH_DECODE)
-      return fail(MQ_INVALID_ARGUMENT, "set_option: force_path must be 0, 2, 3 or 6");
+    if (value != PATH_AUTO && value != PATH_TILED && value != PATH_GENERIC && value != PATH_DECODE &&
+        value != PATH_ROWS)
+      return fail(MQ_INVALID_ARGUMENT, "set_option: force_path must be 0, 2, 3, 6 or 7");
     g_force_path.store((int)value);
     return MQ_SUCCESS;
   }
-  if (std::strcmp(key, "decode_rpw") == 0) {
-    if (value != 0 && value != 1 && value != 2 && value != 4 && value != 8 && value != 16)
-      return fail(MQ_INVALID_ARGUMENT, "set_option: decode_rpw must be 0, 1, 2, 4, 8 or 16");
-    g_dec_rpw.store((int)value);
+  if (std::strcmp(key, "gemv_debug") == 0) {
+    mq::g_gemv_debug = (int)value;
     return MQ_SUCCESS;
   }
-  if (std::strcmp(key, "decode_max_nw") == 0) {
-    if (value != 4 && value != 8 && value != 16)
-      return fail(MQ_INVALID_ARGUMENT, "set_option: decode_max_nw must be 4, 8 or 16");
-    g_dec_nw.store((int)value);
+  if (std::strcmp(key, "gemv_steps") == 0) {
+    if (value < 0 || value > 8) return fail(MQ_INVALID_ARGUMENT, "set_option: gemv_steps must be 0..8");
+    g_gemv_steps.store((int)value);
     return MQ_SUCCESS;
   }
-  if (std::strcmp(key, "decode_wg_per_cu") == 0) {
-    if (value < 1 || value > 8) return fail(MQ_INVALID_ARGUMENT, "set_option: decode_wg_per_cu must be 1..8");
-    g_dec_wpc.store((int)value);
-    return MQ_SUCCESS;
-  }
-  if (std::strcmp(key, "decode_min_chunks") == 0) {
-    if (value < 0 || value > 64) return fail(MQ_INVALID_ARGUMENT, "set_option: decode_min_chunks must be 0..64");
-    g_dec_chunks.store((int)value);
+  if (std::strcmp(key, "gemv_tiles_per_wg") == 0) {
+    if (value != 0 && value != 1 && value != 2 && value != 4)
+      return fail(MQ_INVALID_ARGUMENT, "set_option: gemv_tiles_per_wg must be 0, 1, 2 or 4");
+    g_gemv_tpw.store((int)value);
     return MQ_SUCCESS;
   }
   return fail(MQ_INVALID_ARGUMENT, std::string("set_option: unknown key ") + key);

@@ -151,6 +151,38 @@ __device__ __forceinline__ void mfma_result_fence(f4& v) {
   asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+v"(v));
 }
 
+// ---- buffer loads ----
+// A buffer load whose offset lies outside the descriptor's range returns
+// zeros without touching memory; kOob is such an offset for every range used
+// here (all ranges are below 2^31 bytes).  Loads issued unconditionally this
+// way keep the compiler's load counter exact.
+constexpr uint32_t kOob = 0x80000000u;
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ u4 bload16_nt(rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2));
+}
+__device__ __forceinline__ u4 bload16(rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+__device__ __forceinline__ uint16_t bload2h(rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(uint16_t, __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0));
+}
+__device__ __forceinline__ uint32_t bload2(rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+}
+
+__device__ __forceinline__ float ld_coherent(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+// 8 halves of padding after every 128 activations: the K shifts and lane
+// groups of one wave read fall in different LDS banks.
+__device__ __forceinline__ int xswz(int k) { return k + ((k >> 7) << 3); }
+
+
 __device__ __forceinline__ float silu_f32(float v) { return v / (1.0f + expf(-v)); }
 
 // Scalar dequant of one element (generic kernels).

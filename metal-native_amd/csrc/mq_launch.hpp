@@ -28,23 +28,35 @@ struct LinearArgs {
   int F;                // SwiGLU half width (N = 2F), 0 otherwise
 };
 
-// Persistent row-range GEMV (decode, M <= 16).
-struct DecodeTuning {
-  int rpw = 0;           // weight rows per MFMA tile (0 = from M and K)
-  int max_nw = 16;       // wavefronts per workgroup
-  int wg_per_cu = 1;     // workgroups per CU the rows are spread over
-  int force_chunks = 0;  // tests: stage K in at least this many chunks
+// Split-K MFMA GEMV (decode, M <= 16).
+struct GemvTuning {
+  int steps = 0;   // K steps per wave, 1..8 (0 = planner's choice)
+  int tpw = 0;     // row tiles (= waves) per workgroup: 1, 2 or 4 (0 = planner's choice)
 };
-struct DecodePlan {
-  int rpw, nw, rows_wg, nwg, nsteps, spc, nchunks, xs_stride, xp;
-  uint32_t off_szs, off_red, off_bnd, off_ws;
-  int sz_chunks;
+struct GemvPlan {
+  int rpw, tpw, P, kk, nq, nwg, KS, T, GK, XS;
+  uint32_t off_sz;
+  size_t lds_bytes;
+  size_t cnt_bytes;  // counter region at the start of the workspace
+  size_t ws_bytes;   // 0 when P == 1
+  bool ok;
+};
+extern int g_gemv_debug;  // timing experiments only: 1 skip the split-K reduction, 2 loads only
+bool gemv_supported(const LinearArgs& a);
+GemvPlan gemv_plan(const LinearArgs& a, int num_cus, const GemvTuning& t);
+// ws: ws_bytes of device memory whose first cnt_bytes are zero (the kernel
+// leaves them zero again); calls sharing a workspace must be stream-ordered.
+hipError_t gemv_launch(const LinearArgs& a, const GemvPlan& p, void* ws, hipStream_t s);
+
+// Persistent row-block GEMV (decode with the activations resident in LDS).
+struct RowsPlan {
+  int rpw, nw, nwg, R, TW, KS, XS, maxT, szrows;
+  uint32_t off_sz, off_scr, off_slot;
   size_t lds_bytes;
   bool ok;
 };
-bool decode_supported(const LinearArgs& a);
-DecodePlan decode_plan(const LinearArgs& a, int num_cus, const DecodeTuning& t);
-hipError_t decode_launch(const LinearArgs& a, const DecodePlan& p, hipStream_t s);
+RowsPlan rows_plan(const LinearArgs& a, int num_cus);
+hipError_t rows_launch(const LinearArgs& a, const RowsPlan& p, hipStream_t s);
 
 bool tiled_supported(const LinearArgs& a);
 hipError_t tiled_launch(const LinearArgs& a, hipStream_t s);

@@ -1,0 +1,527 @@
+// Persistent row-block MFMA GEMV for skinny activations whose activation rows
+// fit in LDS (decode; the Qwen2.5-7B down-proj at M = 1 is its main case).
+//
+// Replaces, like mq_gemv.hip, the reference's M<=8 routes
+// (shaders/matmul_dequant_kernel.metal:229-345, :485-576, dispatched at
+// src/ops/matmul.mm:946-1009; shaders/matmul_vecmat_kernel.metal:32-139 for
+// fp16 B [N, K]), computing every row of A.
+//
+// Structure (no synchronisation between workgroups, one launch):
+//  * One workgroup of NW wavefronts per CU.  Workgroup b owns R consecutive
+//    output rows (SwiGLU: R output columns = R gate + R up weight rows) over
+//    the whole of K, so every CU streams the same number of weight bytes.
+//  * Row tile: RPW weight rows x S = 16/RPW K shifts form the 16 columns of the
+//    B operand of v_mfma_f32_16x16x32_f16; one wave load reads RPW rows x 64*S
+//    contiguous bytes.  The A operand holds activation row i % RPW at K shift
+//    i / RPW (needs M <= RPW); the result for (activation i, weight row r) is
+//    sum_s D[s*RPW + i][s*RPW + r].
+//  * The workgroup's work is TW tiles x KS K-steps ("units", tile-major); wave
+//    w takes the contiguous units [w*U/NW, (w+1)*U/NW) and streams them
+//    through a ring of D register slots refilled as they are consumed.  Every
+//    load is an unconditional buffer load (units past the wave's range use an
+//    out-of-range offset), so the load counter is exact and each unit waits
+//    for its own slot only; compute overlaps the stream.
+//  * The activations (all of K, re-ordered for the int4 operand layout) and
+//    the scales/zeros of the workgroup's rows are staged in LDS once.  Their
+//    loads go out first and are waited for after only a short head of the
+//    weight stream: a wave stalls at issue while the memory queues are full,
+//    so a deep stream issued first would hold back the start of compute.
+//  * When a tile ends (or the wave's range does) the wave folds the K shifts
+//    of its accumulator through a per-wave LDS scratch and stores the tile's
+//    M x RPW partial in its own slot.  At the end the workgroup sums, for
+//    each output, the slots of the waves that touched its tile in wave order
+//    (deterministic), applies the epilogue and stores fp16.
+#include "mq_device.hpp"
+#include "mq_launch.hpp"
+
+#include <algorithm>
+#include <cmath>
+
+// Timing probe points; empty unless a benchmark harness defines MQ_TRACE.
+#ifndef MQ_TRACE
+#define MQ_TRACE(slot)
+#endif
+
+namespace mq {
+namespace {
+
+#ifndef MQ_ROWS_KD
+#define MQ_ROWS_KD 4
+#endif
+#ifndef MQ_ROWS_KPRE
+#define MQ_ROWS_KPRE 2
+#endif
+constexpr int kD = MQ_ROWS_KD;     // ring depth (units in flight per wave)
+#ifndef MQ_ROWS_NW
+#define MQ_ROWS_NW 12
+#endif
+constexpr int kNW = MQ_ROWS_NW;  // wavefronts per workgroup
+constexpr int kPre = MQ_ROWS_KPRE;  // ring slots issued before the staging data is waited for
+constexpr int kXB = 8;           // activation pieces per thread per staging batch
+constexpr int kSB = 4;           // scale entries per thread per staging batch
+constexpr size_t kLds = 163840;  // LDS per CU on gfx950
+
+struct RowsKArgs {
+  const _Float16* A; int64_t lda;
+  const unsigned char* W; int64_t ldw;
+  const _Float16* scales; const _Float16* zeros; const _Float16* bias;
+  _Float16* C; int64_t ldc;
+  int M, K, N, F, G, gshift;
+  int R;          // output rows (SwiGLU: output columns) per workgroup
+  int TW;         // row tiles per workgroup
+  int KS;         // K steps per row
+  int XS;         // LDS activation row stride (halves)
+  int maxT;       // partial slots per wave
+  int szrows;     // weight rows whose scales are staged (R, or 2R for SwiGLU)
+  uint32_t off_sz, off_scr, off_slot;  // LDS byte offsets
+  uint32_t a_bytes, sz_bytes, z_bytes;
+  uint64_t ppr_magic, g_magic;  // ceil(2^32 / d): idx / d = (idx * magic) >> 32 for the staged index ranges
+  int dbg;
+};
+
+template <int FMT, int EPI, int RPW>
+__global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
+  constexpr int S = 16 / RPW;
+  constexpr int KPL = FmtTraits<FMT>::KPL;       // k per 16-byte piece
+  constexpr int KSTEP = 4 * KPL * S;             // k per row per unit
+  constexpr int NJ = KPL / 8;                    // MFMAs per unit
+  constexpr int HALF = RPW / 2;
+  constexpr int BPK2 = (FMT == FMT_INT4) ? 1 : (FMT == FMT_INT8 ? 2 : 4);  // 2 x bytes per k
+  extern __shared__ __align__(16) unsigned char smem[];
+
+  constexpr int NW = kNW;
+  constexpr int NT = 64 * kNW;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int M = p.M, KS = p.KS;
+  const int b = blockIdx.x;
+
+  _Float16* xs = (_Float16*)smem;                     // [M][XS]
+  uint32_t* szl = (uint32_t*)(smem + p.off_sz);       // [szrows][G]: s | z << 16
+  float* scr = (float*)(smem + p.off_scr) + w * 256;  // per wave [16][16]
+  float* slots = (float*)(smem + p.off_slot);         // [NW][maxT][M*RPW]
+
+  const int nl = lane & 15, gi = lane >> 4;
+  const int r = nl % RPW, sh = nl / RPW;              // weight row in tile, K shift
+  const int klane = sh * 4 * KPL + gi * KPL;          // this lane's k within a unit
+  MQ_TRACE(0);
+
+  // ---- this workgroup's weight rows ----
+  // local weight row lr: plain lr = t*RPW + r (global row0 + lr); SwiGLU the
+  // tile holds gate columns c = t*HALF + r (r < HALF) and the matching up
+  // rows, local rows c and R + c (global f0 + c and F + f0 + c).
+  const int row0 = b * p.R;
+  int valid;
+  uint32_t span;
+  if (EPI == EPI_SWIGLU) {
+    valid = max(0, min(p.R, p.F - row0));
+    span = (uint32_t)((p.F + valid) * p.ldw);
+  } else {
+    valid = max(0, min(p.R, p.N - row0));
+    span = (uint32_t)(valid * p.ldw);
+  }
+  const rsrc_t wr = make_rsrc(p.W + (int64_t)row0 * p.ldw, span);
+  auto sz_row = [&](int t) -> int {  // this lane's local weight row of tile t
+    if (EPI == EPI_SWIGLU) {
+      const int c = t * HALF + (r % HALF);
+      return (r < HALF) ? c : p.R + c;
+    }
+    return t * RPW + r;
+  };
+  auto row_off = [&](int t) -> uint32_t {  // byte offset of this lane's row of tile t, or kOob
+    if (EPI == EPI_SWIGLU) {
+      const int c = t * HALF + (r % HALF);
+      if (c >= valid) return kOob;
+      return (uint32_t)(((r < HALF) ? c : p.F + c) * p.ldw);
+    } else {
+      const int lr = t * RPW + r;
+      return lr < valid ? (uint32_t)(lr * p.ldw) : kOob;
+    }
+  };
+
+  // ---- unit range of this wave and the ring ----
+  const int U = p.TW * KS;
+  const int u0 = (w * U) / NW;   // NW is a compile-time constant: no division instruction
+  const int nu = ((w + 1) * U) / NW - u0;
+  int lt = u0 / KS, lj = u0 - lt * KS;   // load cursor (tile, step)
+  int left = nu;                          // units the load cursor has not issued
+  uint32_t lro = row_off(lt);             // lane's row offset in tile lt
+  int lk = lj * KSTEP + klane;            // lane's k at the load cursor
+  auto wload = [&]() -> u4 {
+    uint32_t off = kOob;
+    if (left > 0) {
+      if (lk < p.K && lro != kOob) off = lro + (uint32_t)(lk * BPK2 / 2);
+      --left;
+      lk += KSTEP;
+      if (++lj == KS) { lj = 0; ++lt; lk = klane; lro = row_off(lt); }
+    }
+    return bload16_nt(wr, off);
+  };
+
+  // ---- staging loads, issued before the ring: the load counter completes
+  // in order, so staging data loaded after the ring would wait for it ----
+  const rsrc_t ar = make_rsrc(p.A, p.a_bytes);
+  const int ppr = KS * KSTEP / 8;   // whole units: k past K is staged as zeros
+  const int npieces = M * ppr;
+  // exact batch sizes: every load instruction costs texture-unit time, even
+  // one whose lanes are all out of range
+  const int nxb = min(kXB, (npieces + NT - 1) / NT);
+  auto x_fetch = [&](int base, u4* v, int cnt) {
+#pragma unroll
+    for (int e = 0; e < kXB; ++e) {
+      if (e < cnt) {
+        const int idx = base + tid + e * NT;
+        const int i = (int)(((uint64_t)(uint32_t)idx * p.ppr_magic) >> 32), c = idx - i * ppr;
+        v[e] = bload16(ar, (idx < npieces && 8 * c < p.K) ? (uint32_t)((i * p.lda + 8 * c) * 2) : kOob);
+      }
+    }
+  };
+  auto x_put = [&](int base, const u4* v, int cnt) {
+#pragma unroll
+    for (int e = 0; e < kXB; ++e) {
+      const int idx = base + tid + e * NT;
+      if (e < cnt && idx < npieces) {
+        const int i = (int)(((uint64_t)(uint32_t)idx * p.ppr_magic) >> 32), c = idx - i * ppr;
+        u4 vv = v[e];
+        if (FMT == FMT_INT4) vv = perm8_int4(vv);
+        *(u4*)(xs + i * p.XS + xswz(8 * c)) = vv;
+      }
+    }
+  };
+  // scales/zeros of the workgroup's rows, [szrows][G] as s | z << 16
+  const rsrc_t sr = make_rsrc(p.scales, p.sz_bytes);
+  const rsrc_t zr = make_rsrc(p.zeros, p.z_bytes);
+  const int G = p.G;
+  const int nsz = FMT != FMT_F16 ? p.szrows * G : 0;
+  const int nsb = min(kSB, (nsz + NT - 1) / NT);
+  auto s_fetch = [&](int base, uint16_t* sv, uint16_t* zv, int cnt) {
+#pragma unroll
+    for (int e = 0; e < kSB; ++e) {
+      if (e < cnt) {
+        const int idx = base + tid + e * NT;
+        const int lr = (int)(((uint64_t)(uint32_t)idx * p.g_magic) >> 32), g = idx - lr * G;
+        int grow;
+        bool ok;
+        if (EPI == EPI_SWIGLU) {
+          const int c = lr < p.R ? lr : lr - p.R;
+          ok = c < valid;
+          grow = lr < p.R ? row0 + c : p.F + row0 + c;
+        } else {
+          ok = lr < valid;
+          grow = row0 + lr;
+        }
+        const uint32_t off = (ok && idx < nsz) ? (uint32_t)((grow * G + g) * 2) : kOob;
+        sv[e] = bload2h(sr, off);
+        zv[e] = bload2h(zr, off);
+      }
+    }
+  };
+  auto s_put = [&](int base, const uint16_t* sv, const uint16_t* zv, int cnt) {
+#pragma unroll
+    for (int e = 0; e < kSB; ++e) {
+      const int idx = base + tid + e * NT;
+      if (e < cnt && idx < nsz) szl[idx] = (uint32_t)sv[e] | ((uint32_t)zv[e] << 16);
+    }
+  };
+
+  u4 raw[kD];
+  {
+    u4 xv[kXB];
+    uint16_t sv[kSB], zv[kSB];
+    x_fetch(0, xv, nxb);
+    if (FMT != FMT_F16) s_fetch(0, sv, zv, nsb);
+    // every wave's staging loads reach the texture unit first (a plain
+    // barrier: it does not wait for the loads) ...
+    __builtin_amdgcn_s_barrier();
+    MQ_TRACE(5);
+    // ... then a short head of the weight stream.  The staging data is waited
+    // for before the rest: a wave blocks while the memory queues are full, so
+    // a deep stream issued first would hold back the start of compute.
+#pragma unroll
+    for (int d = 0; d < kPre; ++d) raw[d] = wload();
+#pragma unroll
+    for (int e = 0; e < kXB; ++e) asm volatile("" : "+v"(xv[e]));
+#pragma unroll
+    for (int e = 0; e < kSB; ++e) asm volatile("" : "+v"(sv[e]), "+v"(zv[e]));
+    MQ_TRACE(6);
+    x_put(0, xv, nxb);
+    if (FMT != FMT_F16) s_put(0, sv, zv, nsb);
+#pragma unroll
+    for (int d = kPre; d < kD; ++d) raw[d] = wload();
+    MQ_TRACE(7);
+  }
+  // the rest (large M*K, many scale rows) after the ring
+  for (int base = kXB * NT; base < npieces; base += kXB * NT) {
+    u4 xv[kXB];
+    x_fetch(base, xv, kXB);
+    x_put(base, xv, kXB);
+  }
+  for (int base = kSB * NT; base < nsz; base += kSB * NT) {
+    uint16_t sv[kSB], zv[kSB];
+    s_fetch(base, sv, zv, kSB);
+    s_put(base, sv, zv, kSB);
+  }
+  // LDS barrier that leaves the weight loads in flight
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  MQ_TRACE(1);
+
+  // ---- stream ----
+  const int xrow = min(r, M - 1) * p.XS;
+  uint32_t mlo = 0x000F000Fu, mhi = 0x00F000F0u;
+  asm volatile("" : "+v"(mlo), "+v"(mhi));  // keep the nibble masks in VGPRs
+  const uint32_t magic = 0x64006400u;
+
+  int ct = u0 / KS, cj = u0 - ct * KS;   // consume cursor (tile, step)
+  const int ft = ct;                      // first tile of this wave
+  int ck = cj * KSTEP + klane;            // lane's k at the consume cursor
+  int szb = sz_row(ct) * G;               // lane's scale row in LDS
+  const _Float16* xa = xs + xrow + xswz(ck);
+  static_assert(KSTEP % 128 == 0, "the LDS activation padding advances by a constant per unit");
+  constexpr int XADV = KSTEP + (KSTEP >> 7) * 8;
+  f4 acc = (f4){0.f, 0.f, 0.f, 0.f};
+
+  auto flush = [&]() {
+    mfma_result_fence(acc);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) scr[(4 * gi + e) * 16 + nl] = acc[e];
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    if (lane < M * RPW) {
+      const int i = lane / RPW, rr = lane - i * RPW;
+      float v = 0.f;
+#pragma unroll
+      for (int s = 0; s < S; ++s) v += scr[(s * RPW + i) * 16 + s * RPW + rr];
+      slots[(w * p.maxT + (ct - ft)) * (M * RPW) + lane] = v;
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    acc = (f4){0.f, 0.f, 0.f, 0.f};
+  };
+
+  auto step = [&](const u4 v) {
+    h2 s2 = (h2){(_Float16)0.f, (_Float16)0.f}, z2 = s2;
+    if (FMT != FMT_F16) {
+      const int g = min(ck >> p.gshift, G - 1);  // k past K: zero weights, any finite scale
+      const uint32_t e = szl[szb + g];
+      s2 = as_h2(__builtin_amdgcn_perm(e, e, 0x01000100u));
+      z2 = as_h2(__builtin_amdgcn_perm(e, e, 0x03020302u));
+    }
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      h8 bq;
+      if (FMT == FMT_INT4) {
+        const uint32_t dw = (j == 0) ? v.x : (j == 1) ? v.y : (j == 2) ? v.z : v.w;
+        bq = dq_int4_dword_perm_r(dw, s2, z2, mlo, mhi, magic);
+      } else if (FMT == FMT_INT8) {
+        const uint32_t d0 = (j == 0) ? v.x : v.z;
+        const uint32_t d1 = (j == 0) ? v.y : v.w;
+        h2 q0, q1, q2, q3;
+        dq_int8_dword(d0, s2, z2, q0, q1);
+        dq_int8_dword(d1, s2, z2, q2, q3);
+        bq.s01 = q0; bq.s23 = q1; bq.s45 = q2; bq.s67 = q3;
+      } else {
+        bq = __builtin_bit_cast(h8, v);
+      }
+      const h8 a = *(const h8*)(xa + 8 * j);
+      acc = mfma16x16x32(a, bq, acc);
+    }
+  };
+
+  for (int base = 0; base < nu; base += kD) {
+#pragma unroll
+    for (int d = 0; d < kD; ++d) {
+      if (base + d < nu) {
+        if (p.dbg == 2) {
+          acc[0] += __builtin_bit_cast(float, raw[d].x ^ raw[d].w);
+        } else {
+          step(raw[d]);
+        }
+        ck += KSTEP;
+        xa += XADV;
+        const bool last = base + d == nu - 1;
+        if (++cj == KS || last) {
+          flush();
+          if (cj == KS) {
+            cj = 0;
+            ++ct;
+            ck = klane;
+            xa = xs + xrow + xswz(klane);
+            szb = sz_row(ct) * G;
+          }
+        }
+      }
+      raw[d] = wload();
+    }
+  }
+  MQ_TRACE(2);
+  __syncthreads();
+  MQ_TRACE(3);
+
+  // ---- sum the slots per output, epilogue ----
+  const int MR = M * RPW;
+  auto tile_sum = [&](int t, int i, int rr) -> float {
+    float v = 0.f;
+    const int ub = t * KS, ue = ub + KS;
+    for (int ww = 0; ww < NW; ++ww) {
+      const int a0 = (ww * U) / NW, a1 = ((ww + 1) * U) / NW;
+      if (a0 < ue && a1 > ub && a1 > a0) v += slots[(ww * p.maxT + (t - a0 / KS)) * MR + i * RPW + rr];
+    }
+    return v;
+  };
+  if (EPI == EPI_SWIGLU) {
+    for (int idx = tid; idx < M * valid; idx += NT) {
+      const int i = idx / valid, c = idx - i * valid;
+      const int t = c / HALF, rr = c - t * HALF;
+      const float gv = (float)(_Float16)tile_sum(t, i, rr);
+      const float uv = (float)(_Float16)tile_sum(t, i, rr + HALF);
+      p.C[(int64_t)i * p.ldc + row0 + c] = (_Float16)(silu_f32(gv) * uv);
+    }
+  } else {
+    for (int idx = tid; idx < M * valid; idx += NT) {
+      const int i = idx / valid, lr = idx - i * valid;
+      const int t = lr / RPW, rr = lr - t * RPW;
+      float v = tile_sum(t, i, rr);
+      if (EPI == EPI_BIAS) v += (float)p.bias[row0 + lr];
+      p.C[(int64_t)i * p.ldc + row0 + lr] = (_Float16)v;
+    }
+  }
+  MQ_TRACE(4);
+}
+
+template <int FMT, int EPI, int RPW>
+hipError_t launch3(const RowsKArgs& k, const RowsPlan& pl, hipStream_t s) {
+  static bool attr = false;
+  auto fn = rows_kernel<FMT, EPI, RPW>;
+  if (!attr) {
+    hipError_t e = hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLds);
+    if (e != hipSuccess) return e;
+    attr = true;
+  }
+  hipLaunchKernelGGL(fn, dim3(pl.nwg), dim3(64 * kNW), pl.lds_bytes, s, k);
+  return hipGetLastError();
+}
+
+template <int FMT, int EPI>
+hipError_t launch2(const RowsKArgs& k, const RowsPlan& pl, hipStream_t s) {
+  switch (pl.rpw) {
+    case 1: return EPI == EPI_SWIGLU ? hipErrorInvalidValue : launch3<FMT, EPI, 1>(k, pl, s);
+    case 2: return launch3<FMT, EPI, 2>(k, pl, s);
+    case 4: return launch3<FMT, EPI, 4>(k, pl, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <int FMT>
+hipError_t launch1(const RowsKArgs& k, const RowsPlan& pl, int epi, hipStream_t s) {
+  if (FMT == FMT_F16 || epi == EPI_NONE) return launch2<FMT, EPI_NONE>(k, pl, s);
+  if (epi == EPI_BIAS) return launch2<FMT, EPI_BIAS>(k, pl, s);
+  return launch2<FMT, EPI_SWIGLU>(k, pl, s);
+}
+
+int kpl_of(int fmt) { return fmt == FMT_INT4 ? 32 : (fmt == FMT_INT8 ? 16 : 8); }
+size_t al16(size_t v) { return (v + 15) & ~(size_t)15; }
+int gshift_of(const LinearArgs& a) {
+  if (a.fmt == FMT_F16 || a.G == 1) return 31;
+  for (int b = 0; b < 31; ++b)
+    if (a.g == (1 << b)) return b;
+  return -1;
+}
+int xswz_h(int k) { return k + ((k >> 7) << 3); }
+int szrows_of(const LinearArgs& a, int R) { return a.epi == EPI_SWIGLU ? 2 * R : R; }
+
+}  // namespace
+
+RowsPlan rows_plan(const LinearArgs& a, int num_cus) {
+  RowsPlan p{};
+  p.ok = false;
+  const int kpl = kpl_of(a.fmt);
+  if (a.M < 1 || a.M > 4) return p;
+  if (a.K % kpl != 0 || (a.K & 7)) return p;
+  if (a.fmt != FMT_F16 && a.G != 1 && (gshift_of(a) < 0 || a.g < kpl)) return p;
+  if (((uintptr_t)a.W & 15) || (a.ldw & 15)) return p;
+  if (((uintptr_t)a.A & 15) || (a.lda & 7)) return p;
+  if (a.epi == EPI_SWIGLU && a.F * 2 != a.N) return p;
+  const int64_t lim = (int64_t)1 << 31;
+  if (((int64_t)(a.M - 1) * a.lda + a.K) * 2 >= lim) return p;
+  if ((int64_t)a.N * a.G * 2 >= lim) return p;
+  const bool quant = a.fmt != FMT_F16;
+  const int nrows = a.epi == EPI_SWIGLU ? a.F : a.N;
+  // the tile width (>= M rows) with the least padded work per CU: rows per
+  // workgroup rounded up to whole tiles, times K rounded up to whole steps
+  int rpw = 4;
+  double best_work = 1e300;
+  for (int cand = 1; cand <= 4; cand <<= 1) {
+    if (cand < a.M || (a.epi == EPI_SWIGLU && cand < 2)) continue;
+    const int ks = 4 * kpl * (16 / cand);
+    const int gr = a.epi == EPI_SWIGLU ? cand / 2 : cand;
+    const int rr = ((nrows + num_cus - 1) / num_cus + gr - 1) / gr * gr;
+    const double work = (double)rr * ((a.K + ks - 1) / ks * ks) * (1.0 + 0.01 * cand);
+    if (work < best_work) { best_work = work; rpw = cand; }
+  }
+  const int S = 16 / rpw;
+  const int kstep = 4 * kpl * S;
+  const int gran = a.epi == EPI_SWIGLU ? rpw / 2 : rpw;  // output rows per tile
+  // rows per workgroup: a whole number of tiles, one workgroup per CU
+  int R = (nrows + num_cus - 1) / num_cus;
+  R = (R + gran - 1) / gran * gran;
+  const int nwg = (nrows + R - 1) / R;
+  const int TW = R / gran;
+  const int KS = (a.K + kstep - 1) / kstep;
+  const int U = TW * KS;
+  const int nw = kNW;
+  const int per = (U + nw - 1) / nw;
+  const int maxT = per / KS + 2;
+  if ((int64_t)(a.epi == EPI_SWIGLU ? a.F + R : R) * a.ldw >= lim) return p;
+  int XS = xswz_h(KS * kstep) + 8;
+  XS = (XS + 127) / 128 * 128 + 64;  // rows of A fall 128 bytes apart in the LDS banks
+  size_t off = al16((size_t)a.M * XS * 2);
+  const int szrows = a.epi == EPI_SWIGLU ? 2 * R : R;
+  p.off_sz = (uint32_t)off;
+  off += quant ? al16((size_t)szrows * a.G * 4) : 0;
+  p.off_scr = (uint32_t)off;
+  off += (size_t)nw * 256 * 4;
+  p.off_slot = (uint32_t)off;
+  off += al16((size_t)nw * maxT * a.M * rpw * 4);
+  if (off > kLds) return p;
+  if ((int64_t)U * nw >= ((int64_t)1 << 31)) return p;  // unit ranges in 32-bit arithmetic
+  {
+    // idx / d = (idx * ceil(2^32/d)) >> 32 is exact while idx * e < 2^32,
+    // e = ceil(2^32/d)*d - 2^32 < d; the staged index ranges are far below
+    const uint64_t ppr = (uint64_t)KS * kstep / 8;
+    const uint64_t n_x = (uint64_t)a.M * ppr, n_s = (uint64_t)szrows_of(a, R) * a.G;
+    if (n_x * ppr >= (1ull << 32) || n_s * (uint64_t)a.G >= (1ull << 32)) return p;
+  }
+  p.rpw = rpw; p.nw = nw; p.nwg = nwg; p.R = R; p.TW = TW; p.KS = KS; p.XS = XS; p.maxT = maxT;
+  p.szrows = szrows;
+  p.lds_bytes = off;
+  p.ok = true;
+  return p;
+}
+
+hipError_t rows_launch(const LinearArgs& a, const RowsPlan& pl, hipStream_t s) {
+  if (!pl.ok) return hipErrorInvalidValue;
+  RowsKArgs k{};
+  k.A = (const _Float16*)a.A; k.lda = a.lda;
+  k.W = (const unsigned char*)a.W; k.ldw = a.ldw;
+  k.scales = (const _Float16*)a.scales; k.zeros = (const _Float16*)a.zeros;
+  k.bias = (const _Float16*)a.bias;
+  k.C = (_Float16*)a.C; k.ldc = a.ldc;
+  k.M = a.M; k.K = a.K; k.N = a.N; k.F = a.F; k.G = a.G;
+  k.gshift = gshift_of(a);
+  k.R = pl.R; k.TW = pl.TW; k.KS = pl.KS; k.XS = pl.XS; k.maxT = pl.maxT; k.szrows = pl.szrows;
+  k.off_sz = pl.off_sz; k.off_scr = pl.off_scr; k.off_slot = pl.off_slot;
+  k.a_bytes = (uint32_t)(((int64_t)(a.M - 1) * a.lda + a.K) * 2);
+  k.sz_bytes = a.fmt == FMT_F16 ? 0u : (uint32_t)(((int64_t)a.N * a.G * 2 + 3) & ~(int64_t)3);
+  k.z_bytes = a.zeros ? k.sz_bytes : 0u;
+  k.dbg = g_gemv_debug;
+  {
+    const uint64_t ppr = (uint64_t)pl.KS * (4 * kpl_of(a.fmt) * (16 / pl.rpw)) / 8;
+    k.ppr_magic = ((1ull << 32) + ppr - 1) / ppr;
+    k.g_magic = ((1ull << 32) + (uint64_t)a.G - 1) / (uint64_t)a.G;  // 2^32 for G == 1
+  }
+  switch (a.fmt) {
+    case FMT_INT4: return launch1<FMT_INT4>(k, pl, a.epi, s);
+    case FMT_INT8: return launch1<FMT_INT8>(k, pl, a.epi, s);
+    default: return launch1<FMT_F16>(k, pl, a.epi, s);
+  }
+}
+
+}  // namespace mq

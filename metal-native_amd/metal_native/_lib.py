@@ -27,7 +27,7 @@ EPILOGUE_NONE = 0
 EPILOGUE_BIAS = 1
 EPILOGUE_SWIGLU = 2
 
-PATH_NAMES = {0: "none", 2: "tiled", 3: "generic", 4: "vecmat_kn", 6: "decode"}
+PATH_NAMES = {0: "none", 2: "tiled", 3: "generic", 4: "vecmat_kn", 6: "decode", 7: "rows"}
 
 _c_void_p = ctypes.c_void_p
 _i64 = ctypes.c_int64

@@ -70,8 +70,8 @@ def test_validation_without_gpu(lib):
 def test_set_option(lib):
     assert lib.mq_set_option(b"force_path", 9) == 4
     assert lib.mq_set_option(b"force_path", 1) == 4  # retired path id
-    assert lib.mq_set_option(b"decode_rpw", 3) == 4
-    assert lib.mq_set_option(b"decode_max_nw", 2) == 4
+    assert lib.mq_set_option(b"gemv_steps", 9) == 4
+    assert lib.mq_set_option(b"gemv_tiles_per_wg", 3) == 4
     assert lib.mq_set_option(b"nonsense", 1) == 4
     assert b"unknown key" in lib.mq_last_error()
     assert lib.mq_set_option(b"force_path", 0) == 0

@@ -25,7 +25,7 @@ TOL_ABS = 1e-2
 TOL_REL = 1e-3
 GOLD = os.path.join(os.path.dirname(__file__), "golden", "known_answers.npz")
 
-PATHS = {"tiled": 2, "generic": 3, "decode": 6}
+PATHS = {"tiled": 2, "generic": 3, "decode": 6, "rows": 7}
 
 
 @pytest.fixture(scope="module")
@@ -108,7 +108,7 @@ def golden_cases():
     return g, sorted({k.split("/")[0] for k in g.files})
 
 
-@pytest.mark.parametrize("path", [None, "decode", "tiled", "generic"])
+@pytest.mark.parametrize("path", [None, "rows", "decode", "tiled", "generic"])
 def test_known_answers(mn, gpu, path):
     gold, names = golden_cases()
     h = lambda k: gold[k].view(np.float16)
@@ -139,18 +139,18 @@ SMALL = [
 ]
 
 
-@pytest.mark.parametrize("path", [None, "decode", "tiled"])
+@pytest.mark.parametrize("path", [None, "rows", "decode", "tiled"])
 @pytest.mark.parametrize("M,K,N,g", SMALL)
 def test_int4_random(mn, gpu, path, M, K, N, g):
     say(f"int4 M={M} K={K} N={N} g={g} path={path}")
     x, wp, s, z = O.make_int4_problem(M, K, N, g, seed=M * 7 + K + N)
     ref = O.matmul_f32acc(x, O.dequant_int4(wp, s, z, K, g))
     y, taken = run_dm(mn, gpu, x, wp, s, z, g, "int4", path)
-    expect_path(path, taken, shape_ok=not (path == "decode" and M > 16))
+    expect_path(path, taken, shape_ok=not ((path == "decode" and M > 16) or (path == "rows" and M > 4)))
     check_close(y, ref, f"int4 {M}x{K}x{N} g{g} [{taken}]")
 
 
-@pytest.mark.parametrize("path", [None, "decode", "tiled"])
+@pytest.mark.parametrize("path", [None, "rows", "decode", "tiled"])
 @pytest.mark.parametrize("M,K,N", [(1, 256, 64), (4, 512, 96), (16, 1024, 128), (64, 512, 192),
                                    (100, 256, 160)])
 def test_int8_random(mn, gpu, path, M, K, N):
@@ -159,7 +159,7 @@ def test_int8_random(mn, gpu, path, M, K, N):
     zz = (np.random.default_rng(1).uniform(-0.01, 0.01, s.shape)).astype(np.float16)  # exercise zeros
     ref = O.matmul_f32acc(x, O.dequant_int8(q, s, zz, K, g))
     y, taken = run_dm(mn, gpu, x, q, s, zz, g, "int8", path)
-    expect_path(path, taken, shape_ok=not (path == "decode" and M > 16))
+    expect_path(path, taken, shape_ok=not ((path == "decode" and M > 16) or (path == "rows" and M > 4)))
     check_close(y, ref, f"int8 {M}x{K}x{N} [{taken}]")
 
 
@@ -173,7 +173,7 @@ def test_unaligned_shapes(mn, gpu, M, K, N):
     check_close(y, ref, f"unaligned int4 {M}x{K}x{N} [{taken}]")
 
 
-@pytest.mark.parametrize("path", [None, "decode", "tiled", "generic"])
+@pytest.mark.parametrize("path", [None, "rows", "decode", "tiled", "generic"])
 @pytest.mark.parametrize("M", [1, 5, 64, 130])
 def test_epilogues(mn, gpu, path, M):
     say(f"epilogues M={M} path={path}")
@@ -197,8 +197,10 @@ def test_config2_qwen7b_down(mn, gpu, M):
     K, N, g = 18944, 3584, 128
     x, wp, s, z = O.make_int4_problem(M, K, N, g, seed=0)
     ref = O.matmul_f32acc(x, O.dequant_int4(wp, s, z, K, g))
-    for path in ("decode", "tiled"):
+    for path in ("rows", "decode", "tiled"):
         y, taken = run_dm(mn, gpu, x, wp, s, z, g, "int4", path)
+        if path == "rows" and taken != "rows":
+            continue  # activations do not fit in LDS at this M
         assert taken == path
         check_close(y, ref, f"config2 M={M} [{path}]")
 
@@ -227,8 +229,10 @@ def test_config4_int8_swiglu(mn, gpu, M):
     K, F = 3584, 18944
     x, q, s, z, g = O.make_int8_problem(M, K, 2 * F, seed=0)
     acc = O.matmul_f32acc(x, O.dequant_int8(q, s, z, K, g))
-    for path in (("decode", "tiled") if M <= 16 else ("tiled",)):
+    for path in (("rows", "decode", "tiled") if M <= 16 else ("tiled",)):
         y, taken = run_dm(mn, gpu, x, q, s, z, g, "int8", path, epilogue="swiglu")
+        if path == "rows" and taken != "rows":
+            continue  # activations do not fit in LDS at this M
         assert y.shape == (M, F) and taken == path
         check_swiglu(y, acc, f"config4 M={M} [{path}]")
 
@@ -315,7 +319,7 @@ def test_vecmat_route(mn, gpu, M, K, N, transpose_b):
     b = (rng.standard_normal((N, K) if transpose_b else (K, N)) * 0.05).astype(np.float16)
     got = host(mn.matmul(dev(a, gpu), dev(b, gpu), False, transpose_b))
     ref = a.astype(np.float32) @ (b.T if transpose_b else b).astype(np.float32)
-    assert mn.last_path() in ("decode", "vecmat_kn", "generic")
+    assert mn.last_path() in ("rows", "decode", "vecmat_kn", "generic")
     check_close(got, ref, f"vecmat tb={transpose_b}")
 
 
@@ -411,13 +415,14 @@ DECODE_SHAPES = [
 ]
 
 
-@pytest.mark.parametrize("opts", [{}, {"decode_rpw": 16}, {"decode_max_nw": 4}, {"decode_wg_per_cu": 3},
-                                  {"decode_min_chunks": 3}, {"decode_min_chunks": 7, "decode_max_nw": 8}])
+@pytest.mark.parametrize("opts", [{}, {"gemv_steps": 1}, {"gemv_steps": 8}, {"gemv_tiles_per_wg": 1},
+                                  {"gemv_tiles_per_wg": 2, "gemv_steps": 3}])
 @pytest.mark.parametrize("M,K,N,g,qt,epi", DECODE_SHAPES)
 def test_decode_variants(mn, gpu, opts, M, K, N, g, qt, epi):
-    """The persistent decode GEMV under every layout knob: rows per MFMA
-    tile, wavefronts per workgroup, workgroups per CU (tiles shared by
-    several waves) and K staged in several chunks, against the oracle."""
+    """The split-K decode GEMV under its layout knobs (K steps per wave, hence
+    the number of splits; row tiles per workgroup), against the oracle.  A
+    knob the kernel cannot stage for a shape leaves that shape to another
+    kernel, which must still be right."""
     say(f"decode {opts} M={M} K={K} N={N} g={g} {qt} {epi}")
     if qt == "int4":
         x, wp, s, z = O.make_int4_problem(M, K, N, g, seed=K + N + M)
@@ -438,9 +443,20 @@ def test_decode_variants(mn, gpu, opts, M, K, N, g, qt, epi):
     try:
         y, taken = run_dm(mn, gpu, x, wp, s, z, g, qt, "decode", **kw)
     finally:
-        for k, v in {"decode_rpw": 0, "decode_max_nw": 16, "decode_wg_per_cu": 1, "decode_min_chunks": 0}.items():
-            mn.set_option(k, v)
-    assert taken == "decode"
+        for k in opts:
+            mn.set_option(k, 0)
+    if not opts:
+        assert taken == "decode"
+    # the row-block kernel on the same shapes (where its activations fit in LDS)
+    if not opts:
+        y2, taken2 = run_dm(mn, gpu, x, wp, s, z, g, qt, "rows", **kw)
+        if taken2 == "rows":
+            if epi == "swiglu":
+                check_swiglu(y2, acc, "rows")
+            elif epi == "bias":
+                check_close(y2, acc + b.astype(np.float32), "rows bias")
+            else:
+                check_close(y2, acc, "rows")
     if epi == "swiglu":
         check_swiglu(y, acc, f"decode {opts}")
     elif epi == "bias":
