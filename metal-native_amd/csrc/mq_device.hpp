@@ -24,6 +24,7 @@ namespace mq {
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
+typedef float f16v __attribute__((ext_vector_type(16)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 
 
@@ -164,6 +165,9 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
 __device__ __forceinline__ u4 bload16_nt(rsrc_t r, uint32_t off) {
   return __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2));
 }
+__device__ __forceinline__ uint64_t bload8_nt(rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 2));
+}
 __device__ __forceinline__ u4 bload16(rsrc_t r, uint32_t off) {
   return __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }
@@ -182,6 +186,10 @@ __device__ __forceinline__ float ld_coherent(const float* p) {
 // groups of one wave read fall in different LDS banks.
 __device__ __forceinline__ int xswz(int k) { return k + ((k >> 7) << 3); }
 
+
+__device__ __forceinline__ void mfma_result_fence16(f16v& v) {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+v"(v));
+}
 
 __device__ __forceinline__ float silu_f32(float v) { return v / (1.0f + expf(-v)); }
 

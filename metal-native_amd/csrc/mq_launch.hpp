@@ -58,6 +58,13 @@ struct RowsPlan {
 RowsPlan rows_plan(const LinearArgs& a, int num_cus);
 hipError_t rows_launch(const LinearArgs& a, const RowsPlan& p, hipStream_t s);
 
+// 32x32x16 MFMA GEMM with register-ring prefetch (prefill).
+extern int g_gemm_pf;     // K-tiles in flight ahead of the MFMAs (2, 4 or 8)
+extern int g_gemm_waves;  // wavefronts per workgroup for 128-row tiles (4 or 8)
+bool gemm_supported(const LinearArgs& a);
+hipError_t gemm_launch(const LinearArgs& a, hipStream_t s);
+
+// 16x16x32 MFMA GEMM, K steps of 32 (fallback for shapes the GEMM above does not take).
 bool tiled_supported(const LinearArgs& a);
 hipError_t tiled_launch(const LinearArgs& a, hipStream_t s);
 
