@@ -42,6 +42,25 @@ CACHE_BYTES = 256 * 2**20
 ROTATE_TARGET = int(1.3 * CACHE_BYTES)
 
 
+KERNEL_DESC = {
+    "rows": "persistent row-block dequant GEMV, v_mfma_f32_16x16x32_f16, fp32 accumulation",
+    "decode": "split-K dequant GEMV, v_mfma_f32_16x16x32_f16, fp32 accumulation",
+    "tiled": "dequant GEMM, v_mfma_f32_32x32x16_f16, fp32 accumulation",
+}
+TRAFFIC_JSON = os.path.join(ROOT, "profiles", "traffic_rows_kernel_cfg2_m1.json")
+
+
+def traffic_bytes():
+    """HBM bytes per launch of the headline kernel, from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (each counter scaled by what it
+    reads for a plain copy of known size).  None when no summary exists."""
+    try:
+        with open(TRAFFIC_JSON) as f:
+            return json.load(f).get("traffic_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
@@ -167,7 +186,7 @@ def measure(name, steps, warmup, device):
 # CPU baseline: the oracle on this host
 # --------------------------------------------------------------------------
 
-def cpu_baseline(reps: int = 3):
+def cpu_baseline(reps: int = 10):
     import numpy as np
 
     from oracle import mq_oracle as O
@@ -236,8 +255,9 @@ def main():
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--cpu-reps", type=int, default=3)
+    ap.add_argument("--cpu-reps", type=int, default=10)
     ap.add_argument("--only", default=None, help="comma-separated config names (headline always runs)")
+    ap.add_argument("--only-headline", action="store_true", help="measure the headline config only")
     ap.add_argument("--copy-calib", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy (rocprof counter calibration)")
     args = ap.parse_args()
@@ -259,7 +279,9 @@ def main():
         copy_calibration(device)
         return
     names = list(CONFIGS)
-    if args.only:
+    if args.only_headline:
+        names = [HEADLINE]
+    elif args.only:
         want = set(args.only.split(",")) | {HEADLINE}
         names = [n for n in names if n in want]
     results = {}
@@ -293,7 +315,7 @@ def main():
                 "zero-points U{0..15}, x ~ N(0,1))",
         "config": {
             "workload": "BASELINE config 2: Qwen2.5-7B down-proj int4 g128 dequant-GEMV, M=1, K=18944, N=3584",
-            "kernel": "skinny split-K MFMA (v_mfma_f32_16x16x32_f16), fp32 accumulation",
+            "kernel": head["kernel_path"] + " (" + KERNEL_DESC.get(head["kernel_path"], "?") + ")",
             "weights_rotated": head["copies_rotated"],
             "working_set_MB": head["working_set_MB"],
         },
@@ -303,7 +325,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic_bytes(),
         },
         "cpu_baseline": cpu,
         "extra": results,

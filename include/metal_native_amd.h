@@ -97,13 +97,16 @@ MQ_API int mq_swiglu_f16(const void* gate, const void* up, void* out, int64_t n,
  * counterpart).  Keys: "force_path" (0 automatic, 2 tiled MFMA GEMM,
  * 3 generic, 6 decode GEMV), "gemv_steps" (K steps per wavefront of the
  * decode GEMV, 1..8, 0 automatic), "gemv_tiles_per_wg" (row tiles per
- * workgroup: 1, 2 or 4, 0 automatic).  A layout the decode GEMV cannot stage
+ * workgroup: 1, 2 or 4, 0 automatic), "gemm_prefetch" (K-tiles the prefill GEMM loads
+ * ahead: 2, 4 or 8), "gemm_waves" (wavefronts per 128-row GEMM tile: 4 or 8),
+ * force_path 7 selects the row-block decode GEMV.  A layout the decode GEMV cannot stage
  * makes it unavailable (the call then takes the tiled or generic kernel).
  * Returns MQ_INVALID_ARGUMENT for an unknown key or value. */
 MQ_API int mq_set_option(const char* key, int64_t value);
 
 /* Kernel the last successful mq_dequant_matmul / mq_vecmat_f16 call on this
- * thread launched: 2 tiled, 3 generic, 4 vecmat [K,N], 6 decode. */
+ * thread launched: 2 tiled GEMM, 3 generic, 4 vecmat [K,N], 6 split-K decode
+ * GEMV, 7 row-block decode GEMV. */
 MQ_API int mq_last_path(void);
 
 MQ_API const char* mq_last_error(void);

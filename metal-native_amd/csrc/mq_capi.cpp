@@ -288,10 +288,6 @@ MQ_API int mq_set_option(const char* key, int64_t value) {
     mq::g_gemm_waves = (int)value;
     return MQ_SUCCESS;
   }
-  if (std::strcmp(key, "gemv_debug") == 0) {
-    mq::g_gemv_debug = (int)value;
-    return MQ_SUCCESS;
-  }
   if (std::strcmp(key, "gemv_steps") == 0) {
     if (value < 0 || value > 8) return fail(MQ_INVALID_ARGUMENT, "set_option: gemv_steps must be 0..8");
     g_gemv_steps.store((int)value);

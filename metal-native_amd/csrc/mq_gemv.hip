@@ -61,7 +61,6 @@ struct GemvKArgs {
   int GK;       // LDS scale entries per tile row
   uint32_t off_sz;              // LDS byte offset of the scale table
   uint32_t a_bytes, sz_bytes, z_bytes;
-  int dbg;
   float* part;                  // [P][M][T*RPW]
   uint32_t* cnt;                // [nq]
 };
@@ -238,13 +237,6 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvKArgs p) {
     }
   };
 
-  if (p.dbg == 2) {
-    uint32_t xx = 0;
-#pragma unroll
-    for (int d = 0; d < KK; ++d) xx ^= raw[d].x ^ raw[d].w;
-    if (xx == 0x9d3a1f77u) p.C[0] = (_Float16)1.f;
-    return;
-  }
 #pragma unroll
   for (int d = 0; d < KK; ++d) step(raw[d], d);
   mfma_result_fence(acc);
@@ -290,10 +282,6 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvKArgs p) {
   }
 
   // ---- split-K: partials, last-arriver reduction ----
-  if (p.dbg == 1) {
-    if (holder && t < p.T && v[0] == 1234.5f) p.C[0] = (_Float16)v[1];
-    return;
-  }
   // Partials and counters use system-scope (cache-coherent, L2-bypassing)
   // accesses, so no L2 writeback or invalidate is needed anywhere: a
   // workgroup's partial stores are complete (s_waitcnt) before its counter
@@ -403,8 +391,6 @@ int gshift_of(const LinearArgs& a) {
 
 }  // namespace
 
-int g_gemv_debug = 0;
-
 bool gemv_supported(const LinearArgs& a) {
   const int kpl = kpl_of(a.fmt);
   if (a.M < 1 || a.M > 16) return false;
@@ -497,7 +483,6 @@ hipError_t gemv_launch(const LinearArgs& a, const GemvPlan& pl, void* ws, hipStr
   k.C = (_Float16*)a.C; k.ldc = a.ldc;
   k.M = a.M; k.K = a.K; k.N = a.N; k.F = a.F; k.G = a.G;
   k.gshift = gshift_of(a);
-  k.dbg = g_gemv_debug;
   k.T = pl.T; k.nq = pl.nq; k.P = pl.P; k.KS = pl.KS; k.XS = pl.XS; k.GK = pl.GK;
   k.off_sz = pl.off_sz;
   k.a_bytes = (uint32_t)(((int64_t)(a.M - 1) * a.lda + a.K) * 2);

@@ -41,7 +41,6 @@ struct GemvPlan {
   size_t ws_bytes;   // 0 when P == 1
   bool ok;
 };
-extern int g_gemv_debug;  // timing experiments only: 1 skip the split-K reduction, 2 loads only
 bool gemv_supported(const LinearArgs& a);
 GemvPlan gemv_plan(const LinearArgs& a, int num_cus, const GemvTuning& t);
 // ws: ws_bytes of device memory whose first cnt_bytes are zero (the kernel

@@ -76,7 +76,6 @@ struct RowsKArgs {
   uint32_t off_sz, off_scr, off_slot;  // LDS byte offsets
   uint32_t a_bytes, sz_bytes, z_bytes;
   uint64_t ppr_magic, g_magic;  // ceil(2^32 / d): idx / d = (idx * magic) >> 32 for the staged index ranges
-  int dbg;
 };
 
 template <int FMT, int EPI, int RPW>
@@ -329,11 +328,7 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
 #pragma unroll
     for (int d = 0; d < kD; ++d) {
       if (base + d < nu) {
-        if (p.dbg == 2) {
-          acc[0] += __builtin_bit_cast(float, raw[d].x ^ raw[d].w);
-        } else {
-          step(raw[d]);
-        }
+        step(raw[d]);
         ck += KSTEP;
         xa += XADV;
         const bool last = base + d == nu - 1;
@@ -511,7 +506,6 @@ hipError_t rows_launch(const LinearArgs& a, const RowsPlan& pl, hipStream_t s) {
   k.a_bytes = (uint32_t)(((int64_t)(a.M - 1) * a.lda + a.K) * 2);
   k.sz_bytes = a.fmt == FMT_F16 ? 0u : (uint32_t)(((int64_t)a.N * a.G * 2 + 3) & ~(int64_t)3);
   k.z_bytes = a.zeros ? k.sz_bytes : 0u;
-  k.dbg = g_gemv_debug;
   {
     const uint64_t ppr = (uint64_t)pl.KS * (4 * kpl_of(a.fmt) * (16 / pl.rpw)) / 8;
     k.ppr_magic = ((1ull << 32) + ppr - 1) / ppr;
