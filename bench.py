@@ -182,6 +182,31 @@ def measure(name, steps, warmup, device):
     return res
 
 
+def decode_bench(device):
+    """28-layer Qwen2.5-7B-shaped decoder, int4 g128
+    everywhere (lm_head included), batch 1, 512-token random KV cache, greedy
+    decode of 64 tokens, one HIP graph replay per token."""
+    import torch
+
+    from metal_native.decoder import SyntheticDecoder, decode_tokens_per_second, qwen25_7b
+
+    cfg = qwen25_7b()
+    model = SyntheticDecoder(cfg, device, seed=0, prefilled=512)
+    r = decode_tokens_per_second(model, n_tokens=64)
+    per_layer = sum(ql.wp.numel() + 2 * ql.scales.numel() * 2
+                    for L in model.layers for ql in (L["qkv"], L["o"], L["gate_up"], L["down"])) / cfg.layers
+    head = model.lm_head.wp.numel() + 4 * model.lm_head.scales.numel()
+    weight_bytes = per_layer * cfg.layers + head
+    r["weight_bytes_per_token"] = int(weight_bytes)
+    r["weight_stream_GB/s"] = round(weight_bytes / (r["ms_per_token"] * 1e-3) / 1e9, 1)
+    r["floor_ms_per_token_at_8TBps"] = round(weight_bytes / 8e12 * 1e3, 3)
+    r["ms_per_token"] = round(r["ms_per_token"], 4)
+    r["tokens_per_s"] = round(r["tokens_per_s"], 1)
+    del model
+    torch.cuda.empty_cache()
+    return r
+
+
 # --------------------------------------------------------------------------
 # CPU baseline: the oracle on this host
 # --------------------------------------------------------------------------
@@ -291,6 +316,14 @@ def main():
         results[n] = measure(n, steps, args.warmup, device)
         log(f"[bench] {n}: {json.dumps(results[n])}")
     head = results[HEADLINE]
+
+    if not args.only_headline and not args.only:
+        try:
+            log("[bench] cfg5 synthetic Qwen2.5-7B decode step ...")
+            results["cfg5_qwen7b_decode_64tok"] = decode_bench(device)
+            log(f"[bench] cfg5: {json.dumps(results['cfg5_qwen7b_decode_64tok'])}")
+        except Exception as e:  # noqa: BLE001  (the headline line must still print)
+            results["cfg5_qwen7b_decode_64tok"] = {"error": repr(e)}
 
     cpu = None
     if not args.no_cpu:

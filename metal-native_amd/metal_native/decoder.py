@@ -1,0 +1,230 @@
+"""Synthetic Qwen2.5-7B-shaped decoder whose every linear layer runs on the
+quantized-linear kernels.
+
+The reference's counterpart is its numpy MiniGPT example
+(examples/llm_generation.py) and the prefill/decode split of PhasePipeline
+(src/inference/phase_pipeline.mm:42-51); neither quantizes.  Here every
+projection is an int4 g128 ``dequant_matmul``:
+
+* q/k/v: one fused call over the concatenated weight rows, with the bias
+  epilogue (Qwen2 attention projections carry biases);
+* o_proj;
+* gate/up: one fused call with the SwiGLU epilogue (gate rows, then up rows);
+* down_proj and the lm_head.
+
+RMSNorm, rotary embedding, grouped-query attention over the KV cache,
+residual adds and the greedy argmax are PyTorch glue on the same stream.  The
+decode step has static shapes (the position is a device tensor and attention
+masks the unused cache slots), so a whole step can be captured in a HIP graph
+and replayed token after token.
+
+Weights are random (no checkpoints are available): int4 nibbles U{0..15},
+scales U(0.005, 0.02), integer zero-points U{0..15} mapped to the reference's
+already-scaled zeros ``half((zp - 8) * s)``; embeddings, norms and biases
+fp16 ~ N(0, 0.02).
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+
+from . import ops
+
+
+@dataclass
+class DecoderConfig:
+    layers: int = 28
+    d: int = 3584
+    heads: int = 28
+    kv_heads: int = 4
+    head_dim: int = 128
+    ffn: int = 18944
+    vocab: int = 152064
+    group_size: int = 128
+    max_len: int = 512 + 64
+    rope_theta: float = 1.0e6
+    eps: float = 1e-6
+
+
+def qwen25_7b(max_len: int = 512 + 64) -> DecoderConfig:
+    return DecoderConfig(max_len=max_len)
+
+
+class QLinear:
+    """int4 g128 weights ``[N, K/2]`` + fp16 scales/zeros ``[N, K/g]``."""
+
+    def __init__(self, wp: torch.Tensor, scales: torch.Tensor, zeros: torch.Tensor, group_size: int,
+                 bias: torch.Tensor | None = None):
+        self.wp, self.scales, self.zeros, self.g, self.bias = wp, scales, zeros, group_size, bias
+
+    @staticmethod
+    def random(n: int, k: int, g: int, gen: torch.Generator, device, bias: bool = False) -> "QLinear":
+        G = (k + g - 1) // g
+        wp = torch.randint(0, 256, (n, k // 2), dtype=torch.uint8, device=device, generator=gen)
+        s = (torch.rand((n, G), device=device, generator=gen) * 0.015 + 0.005).half()
+        zp = torch.randint(0, 16, (n, G), device=device, generator=gen).float()
+        z = ((zp - 8.0) * s.float()).half()
+        b = (torch.randn(n, device=device, generator=gen) * 0.02).half() if bias else None
+        return QLinear(wp, s, z, g, b)
+
+    def __call__(self, x: torch.Tensor, epilogue: str | None = None) -> torch.Tensor:
+        if self.bias is not None and epilogue is None:
+            return ops.dequant_matmul(x, self.wp, self.scales, self.zeros, self.g, "int4",
+                                      epilogue="bias", bias=self.bias)
+        return ops.dequant_matmul(x, self.wp, self.scales, self.zeros, self.g, "int4", epilogue=epilogue)
+
+
+def rms_norm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
+    xf = x.float()
+    return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps) * w.float()).half()
+
+
+def rope_tables(cfg: DecoderConfig, device) -> tuple[torch.Tensor, torch.Tensor]:
+    half = cfg.head_dim // 2
+    inv = 1.0 / (cfg.rope_theta ** (torch.arange(0, half, device=device, dtype=torch.float32) / half))
+    t = torch.arange(cfg.max_len, device=device, dtype=torch.float32)
+    f = torch.outer(t, inv)
+    emb = torch.cat([f, f], dim=-1)
+    return emb.cos(), emb.sin()
+
+
+def apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """x [H, Dh] fp16, cos/sin [Dh] fp32 (rotate-half convention)."""
+    xf = x.float()
+    h = xf.shape[-1] // 2
+    rot = torch.cat([-xf[..., h:], xf[..., :h]], dim=-1)
+    return (xf * cos + rot * sin).half()
+
+
+class SyntheticDecoder:
+    def __init__(self, cfg: DecoderConfig, device, seed: int = 0, prefilled: int = 512):
+        self.cfg = cfg
+        self.device = torch.device(device)
+        gen = torch.Generator(device=self.device)
+        gen.manual_seed(seed)
+        d, g = cfg.d, cfg.group_size
+        nq, nkv = cfg.heads * cfg.head_dim, cfg.kv_heads * cfg.head_dim
+        rn = lambda *s: (torch.randn(*s, device=self.device, generator=gen) * 0.02).half()
+        self.embed = rn(cfg.vocab, d)
+        self.layers = []
+        for _ in range(cfg.layers):
+            self.layers.append({
+                "ln1": rn(d), "ln2": rn(d),
+                "qkv": QLinear.random(nq + 2 * nkv, d, g, gen, self.device, bias=True),
+                "o": QLinear.random(d, nq, g, gen, self.device),
+                "gate_up": QLinear.random(2 * cfg.ffn, d, g, gen, self.device),
+                "down": QLinear.random(d, cfg.ffn, g, gen, self.device),
+            })
+        self.norm = rn(d)
+        self.lm_head = QLinear.random(cfg.vocab, d, g, gen, self.device)
+        self.cos, self.sin = rope_tables(cfg, self.device)
+        # KV cache [layers, 2, kv_heads, max_len, head_dim]; the first `prefilled`
+        # positions hold random keys/values (the benchmark's 512-token cache)
+        self.kv = torch.zeros((cfg.layers, 2, cfg.kv_heads, cfg.max_len, cfg.head_dim),
+                              dtype=torch.float16, device=self.device)
+        if prefilled:
+            self.kv[:, :, :, :prefilled] = (torch.randn((cfg.layers, 2, cfg.kv_heads, prefilled, cfg.head_dim),
+                                                        device=self.device, generator=gen)).half()
+        self.prefilled = prefilled
+        self.positions = torch.arange(cfg.max_len, device=self.device)
+
+    # one decode step: token [1] int64, pos [1] int64 (device tensors) -> next token [1]
+    def step(self, token: torch.Tensor, pos: torch.Tensor, return_logits: bool = False):
+        cfg = self.cfg
+        H, KVH, Dh = cfg.heads, cfg.kv_heads, cfg.head_dim
+        grp = H // KVH
+        x = self.embed.index_select(0, token)                      # [1, d]
+        cos = self.cos.index_select(0, pos)[0]
+        sin = self.sin.index_select(0, pos)[0]
+        mask = torch.where(self.positions <= pos, 0.0, float("-inf")).float()  # [L]
+        scale = 1.0 / math.sqrt(Dh)
+        for li, L in enumerate(self.layers):
+            h = rms_norm(x, L["ln1"], cfg.eps)
+            qkv = L["qkv"](h)[0]                                     # [nq + 2 nkv]
+            q = qkv[:H * Dh].view(H, Dh)
+            k = qkv[H * Dh:(H + KVH) * Dh].view(KVH, Dh)
+            v = qkv[(H + KVH) * Dh:].view(KVH, Dh)
+            q = apply_rope(q, cos, sin)
+            k = apply_rope(k, cos, sin)
+            self.kv[li, 0].index_copy_(1, pos, k.unsqueeze(1))
+            self.kv[li, 1].index_copy_(1, pos, v.unsqueeze(1))
+            kc, vc = self.kv[li, 0], self.kv[li, 1]                # [KVH, L, Dh]
+            qg = q.view(KVH, grp, Dh)
+            s = torch.matmul(qg.float(), kc.float().transpose(1, 2)) * scale + mask  # [KVH, grp, L]
+            p = torch.softmax(s, dim=-1)
+            a = torch.matmul(p, vc.float()).half().reshape(1, H * Dh)
+            x = x + L["o"](a)
+            h = rms_norm(x, L["ln2"], cfg.eps)
+            x = x + L["down"](L["gate_up"](h, epilogue="swiglu"))
+        logits = self.lm_head(rms_norm(x, self.norm, cfg.eps))     # [1, vocab]
+        nxt = torch.argmax(logits.float(), dim=-1)
+        return (nxt, logits) if return_logits else nxt
+
+    def reference_step(self, token: int, pos: int, dequant) -> torch.Tensor:
+        """The same step in fp32 torch with weights from ``dequant(qlinear) ->
+        fp16 [N, K]`` (e.g. the CPU oracle); returns logits [vocab] (fp32).
+        Rounds to fp16 where the kernel path does (projection outputs,
+        residual stream, norms), so the two agree within the matmul tolerance."""
+        cfg = self.cfg
+        H, KVH, Dh = cfg.heads, cfg.kv_heads, cfg.head_dim
+        grp = H // KVH
+        dev = self.device
+        lin = lambda ql, x: (x.float() @ dequant(ql).to(dev).float().t())
+        x = self.embed[token:token + 1]
+        cos, sin = self.cos[pos], self.sin[pos]
+        scale = 1.0 / math.sqrt(Dh)
+        kv = self.kv.clone()
+        for li, L in enumerate(self.layers):
+            h = rms_norm(x, L["ln1"], cfg.eps)
+            qkv = (lin(L["qkv"], h) + L["qkv"].bias.float()).half()[0]
+            q = apply_rope(qkv[:H * Dh].view(H, Dh), cos, sin)
+            k = apply_rope(qkv[H * Dh:(H + KVH) * Dh].view(KVH, Dh), cos, sin)
+            v = qkv[(H + KVH) * Dh:].view(KVH, Dh)
+            kv[li, 0, :, pos] = k
+            kv[li, 1, :, pos] = v
+            kc, vc = kv[li, 0, :, :pos + 1].float(), kv[li, 1, :, :pos + 1].float()
+            s = torch.matmul(q.view(KVH, grp, Dh).float(), kc.transpose(1, 2)) * scale
+            a = torch.matmul(torch.softmax(s, dim=-1), vc).half().reshape(1, H * Dh)
+            x = x + lin(L["o"], a).half()
+            h = rms_norm(x, L["ln2"], cfg.eps)
+            gu = lin(L["gate_up"], h).half().float()
+            gate, up = gu[:, :cfg.ffn], gu[:, cfg.ffn:]
+            act = (gate / (1.0 + torch.exp(-gate)) * up).half()
+            x = x + lin(L["down"], act).half()
+        return lin(self.lm_head, rms_norm(x, self.norm, cfg.eps))[0]
+
+
+def decode_tokens_per_second(model: SyntheticDecoder, n_tokens: int = 64, warmup: int = 3) -> dict:
+    """Greedy-decode ``n_tokens`` tokens after the prefilled cache, each step a
+    replay of one captured HIP graph; returns tokens/s and ms/token."""
+    dev = model.device
+    tok = torch.zeros(1, dtype=torch.int64, device=dev)
+    pos = torch.full((1,), model.prefilled, dtype=torch.int64, device=dev)
+    stream = torch.cuda.Stream(dev)
+    stream.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(stream):
+        for _ in range(warmup):  # eager warm-up: kernels loaded, workspaces allocated
+            model.step(tok, pos)
+    torch.cuda.synchronize(dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        nxt = model.step(tok, pos)
+        tok.copy_(nxt)
+        pos.add_(1)
+    pos.fill_(model.prefilled)
+    graph.replay()  # one untimed replay
+    pos.fill_(model.prefilled)
+    torch.cuda.synchronize(dev)
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(n_tokens):
+        graph.replay()
+    t1.record()
+    torch.cuda.synchronize(dev)
+    ms = t0.elapsed_time(t1)
+    return {"tokens": n_tokens, "ms_per_token": ms / n_tokens, "tokens_per_s": n_tokens / (ms / 1000.0),
+            "final_pos": int(pos.item())}
