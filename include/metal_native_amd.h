@@ -93,6 +93,29 @@ MQ_API int mq_vecmat_f16(const void* a, int64_t lda, const void* b, int64_t ldb,
  * _C.fast.swiglu at bindings/bind_ops.cpp:84-93). */
 MQ_API int mq_swiglu_f16(const void* gate, const void* up, void* out, int64_t n, void* stream);
 
+/* Decoder glue for the synthetic decode step.  No
+ * counterpart on the reference's quantized path: its MiniGPT example
+ * (examples/llm_generation.py) does these steps in numpy.
+ * add_rmsnorm: per row, x <- half(x + delta) (delta may be NULL), then
+ *   out = half(x * rsqrt(mean(x^2) + eps) * weight); x, out fp16 [rows, n].
+ * rope_kv: qkv fp16 [heads*D | kv_heads*D | kv_heads*D]; q_out = rope(q);
+ *   k_cache[h, pos] = rope(k), v_cache[h, pos] = v (caches fp16
+ *   [kv_heads, max_len, D]); cos/sin fp32 [max_len, D] (rotate-half); pos is
+ *   a device int64.
+ * attention_decode: out[h] = softmax(q[h] . K^T * scale, t <= pos) . V for
+ *   one query token, head h reading kv head h / (heads / kv_heads); split
+ *   over positions, with per-split partials in the caller's workspace of
+ *   mq_attention_decode_workspace_size(heads, head_dim, max_len) bytes. */
+MQ_API int mq_add_rmsnorm_f16(void* x, const void* delta, const void* weight, void* out, int64_t rows, int64_t n,
+                              float eps, void* stream);
+MQ_API int mq_rope_kv_f16(const void* qkv, const float* cos_table, const float* sin_table, const int64_t* pos,
+                          void* q_out, void* k_cache, void* v_cache, int32_t heads, int32_t kv_heads,
+                          int32_t head_dim, int64_t max_len, void* stream);
+MQ_API int64_t mq_attention_decode_workspace_size(int32_t heads, int32_t head_dim, int64_t max_len);
+MQ_API int mq_attention_decode_f16(const void* q, const void* k_cache, const void* v_cache, const int64_t* pos,
+                                   void* out, int32_t heads, int32_t kv_heads, int32_t head_dim, int64_t max_len,
+                                   float scale, void* workspace, int64_t workspace_bytes, void* stream);
+
 /* Kernel-path override and layout knobs for tests and tuning (no reference
  * counterpart).  Keys: "force_path" (0 automatic, 2 tiled MFMA GEMM,
  * 3 generic, 6 decode GEMV), "gemv_steps" (K steps per wavefront of the

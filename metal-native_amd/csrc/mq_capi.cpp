@@ -268,6 +268,49 @@ MQ_API int mq_swiglu_f16(const void* gate, const void* up, void* out, int64_t n,
   return MQ_SUCCESS;
 }
 
+MQ_API int mq_add_rmsnorm_f16(void* x, const void* delta, const void* weight, void* out, int64_t rows, int64_t n,
+                              float eps, void* stream) {
+  if (!x || !weight || !out) return fail(MQ_INVALID_ARGUMENT, "add_rmsnorm: null pointer argument");
+  if (rows < 1 || n < 1 || rows > INT32_MAX || n > INT32_MAX) return fail(MQ_INVALID_ARGUMENT, "add_rmsnorm: bad shape");
+  hipError_t e = mq::add_rmsnorm_launch(x, delta, weight, out, (int)rows, (int)n, eps, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "add_rmsnorm: kernel launch failed");
+  return MQ_SUCCESS;
+}
+
+MQ_API int mq_rope_kv_f16(const void* qkv, const float* cos_table, const float* sin_table, const int64_t* pos,
+                          void* q_out, void* k_cache, void* v_cache, int32_t heads, int32_t kv_heads,
+                          int32_t head_dim, int64_t max_len, void* stream) {
+  if (!qkv || !cos_table || !sin_table || !pos || !q_out || !k_cache || !v_cache)
+    return fail(MQ_INVALID_ARGUMENT, "rope_kv: null pointer argument");
+  if (heads < 1 || kv_heads < 1 || heads % kv_heads || head_dim < 2 || (head_dim & 1) || max_len < 1)
+    return fail(MQ_INVALID_ARGUMENT, "rope_kv: bad shape");
+  hipError_t e = mq::rope_kv_launch(qkv, cos_table, sin_table, pos, q_out, k_cache, v_cache, heads, kv_heads,
+                                    head_dim, max_len, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "rope_kv: kernel launch failed");
+  return MQ_SUCCESS;
+}
+
+MQ_API int64_t mq_attention_decode_workspace_size(int32_t heads, int32_t head_dim, int64_t max_len) {
+  if (heads < 1 || head_dim < 1 || max_len < 1) return -1;
+  return (int64_t)mq::attn_decode_workspace(heads, head_dim, max_len);
+}
+
+MQ_API int mq_attention_decode_f16(const void* q, const void* k_cache, const void* v_cache, const int64_t* pos,
+                                   void* out, int32_t heads, int32_t kv_heads, int32_t head_dim, int64_t max_len,
+                                   float scale, void* workspace, int64_t workspace_bytes, void* stream) {
+  if (!q || !k_cache || !v_cache || !pos || !out || !workspace)
+    return fail(MQ_INVALID_ARGUMENT, "attention_decode: null pointer argument");
+  if (heads < 1 || kv_heads < 1 || heads % kv_heads || head_dim < 8 || head_dim > 512 || (head_dim & 7) ||
+      max_len < 1)
+    return fail(MQ_INVALID_ARGUMENT, "attention_decode: bad shape");
+  if (workspace_bytes < (int64_t)mq::attn_decode_workspace(heads, head_dim, max_len))
+    return fail(MQ_INVALID_ARGUMENT, "attention_decode: workspace too small");
+  hipError_t e = mq::attn_decode_launch(q, k_cache, v_cache, pos, out, heads, kv_heads, head_dim, max_len, scale,
+                                        workspace, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "attention_decode: kernel launch failed");
+  return MQ_SUCCESS;
+}
+
 MQ_API int mq_set_option(const char* key, int64_t value) {
   if (!key) return fail(MQ_INVALID_ARGUMENT, "set_option: null key");
   if (std::strcmp(key, "force_path") == 0) {

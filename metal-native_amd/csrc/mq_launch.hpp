@@ -80,6 +80,15 @@ struct DequantArgs {
 };
 hipError_t dequantize_launch(const DequantArgs& a, hipStream_t s);
 
+// Decoder glue (synthetic decode step).
+hipError_t add_rmsnorm_launch(void* x, const void* delta, const void* w, void* out, int rows, int n, float eps,
+                              hipStream_t s);
+hipError_t rope_kv_launch(const void* qkv, const float* cos_t, const float* sin_t, const int64_t* pos, void* q_out,
+                          void* kc, void* vc, int H, int KVH, int D, int64_t L, hipStream_t s);
+size_t attn_decode_workspace(int H, int D, int64_t L);
+hipError_t attn_decode_launch(const void* q, const void* kc, const void* vc, const int64_t* pos, void* out, int H,
+                              int KVH, int D, int64_t L, float scale, void* ws, hipStream_t s);
+
 hipError_t swiglu_launch(const void* gate, const void* up, void* out, int64_t n, hipStream_t s);
 
 // fp16 GEMV with B stored [K, N] (transpose_b == false): C = A . B.

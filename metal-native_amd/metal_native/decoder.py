@@ -12,11 +12,12 @@ projection is an int4 g128 ``dequant_matmul``:
 * gate/up: one fused call with the SwiGLU epilogue (gate rows, then up rows);
 * down_proj and the lm_head.
 
-RMSNorm, rotary embedding, grouped-query attention over the KV cache,
-residual adds and the greedy argmax are PyTorch glue on the same stream.  The
-decode step has static shapes (the position is a device tensor and attention
-masks the unused cache slots), so a whole step can be captured in a HIP graph
-and replayed token after token.
+Residual add + RMSNorm, rotary embedding + KV-cache write and single-token
+grouped-query attention are the library's glue kernels (mq_glue.hip); the
+embedding lookup and the greedy argmax are PyTorch ops on the same stream.
+The decode step has static shapes (the position is a device tensor), so a
+whole step is captured in a HIP graph and replayed token after token.
+``reference_step`` restates the step in plain fp32 PyTorch for the tests.
 
 Weights are random (no checkpoints are available): int4 nibbles U{0..15},
 scales U(0.005, 0.02), integer zero-points U{0..15} mapped to the reference's
@@ -133,33 +134,21 @@ class SyntheticDecoder:
 
     # one decode step: token [1] int64, pos [1] int64 (device tensors) -> next token [1]
     def step(self, token: torch.Tensor, pos: torch.Tensor, return_logits: bool = False):
+        """Eight launches per layer: add+RMSNorm, QKV (+bias), RoPE + cache
+        write, attention, o_proj, add+RMSNorm, gate/up (+SwiGLU), down."""
         cfg = self.cfg
         H, KVH, Dh = cfg.heads, cfg.kv_heads, cfg.head_dim
-        grp = H // KVH
-        x = self.embed.index_select(0, token)                      # [1, d]
-        cos = self.cos.index_select(0, pos)[0]
-        sin = self.sin.index_select(0, pos)[0]
-        mask = torch.where(self.positions <= pos, 0.0, float("-inf")).float()  # [L]
         scale = 1.0 / math.sqrt(Dh)
+        x = self.embed.index_select(0, token)                      # [1, d] residual stream
+        delta = None
         for li, L in enumerate(self.layers):
-            h = rms_norm(x, L["ln1"], cfg.eps)
-            qkv = L["qkv"](h)[0]                                     # [nq + 2 nkv]
-            q = qkv[:H * Dh].view(H, Dh)
-            k = qkv[H * Dh:(H + KVH) * Dh].view(KVH, Dh)
-            v = qkv[(H + KVH) * Dh:].view(KVH, Dh)
-            q = apply_rope(q, cos, sin)
-            k = apply_rope(k, cos, sin)
-            self.kv[li, 0].index_copy_(1, pos, k.unsqueeze(1))
-            self.kv[li, 1].index_copy_(1, pos, v.unsqueeze(1))
-            kc, vc = self.kv[li, 0], self.kv[li, 1]                # [KVH, L, Dh]
-            qg = q.view(KVH, grp, Dh)
-            s = torch.matmul(qg.float(), kc.float().transpose(1, 2)) * scale + mask  # [KVH, grp, L]
-            p = torch.softmax(s, dim=-1)
-            a = torch.matmul(p, vc.float()).half().reshape(1, H * Dh)
-            x = x + L["o"](a)
-            h = rms_norm(x, L["ln2"], cfg.eps)
-            x = x + L["down"](L["gate_up"](h, epilogue="swiglu"))
-        logits = self.lm_head(rms_norm(x, self.norm, cfg.eps))     # [1, vocab]
+            h = ops.add_rmsnorm(x, delta, L["ln1"], cfg.eps)        # x += delta; h = norm(x)
+            qkv = L["qkv"](h)
+            q = ops.rope_kv(qkv, self.cos, self.sin, pos, self.kv[li, 0], self.kv[li, 1], H, KVH, Dh)
+            a = ops.attention_decode(q, self.kv[li, 0], self.kv[li, 1], pos, scale)
+            h = ops.add_rmsnorm(x, L["o"](a), L["ln2"], cfg.eps)
+            delta = L["down"](L["gate_up"](h, epilogue="swiglu"))
+        logits = self.lm_head(ops.add_rmsnorm(x, delta, self.norm, cfg.eps))   # [1, vocab]
         nxt = torch.argmax(logits.float(), dim=-1)
         return (nxt, logits) if return_logits else nxt
 

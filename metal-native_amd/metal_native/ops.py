@@ -364,6 +364,51 @@ def swiglu(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
     return out
 
 
+# ---------------------------------------------------------------------------
+# decoder glue (extension: the synthetic decode step of BASELINE config 5)
+# ---------------------------------------------------------------------------
+
+def add_rmsnorm(x: torch.Tensor, delta: torch.Tensor | None, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """``x += delta`` (fp16, in place; skipped when ``delta`` is None), then
+    returns ``half(x * rsqrt(mean(x^2) + eps) * weight)`` per row."""
+    for t, what in ((x, "x"), (weight, "weight")):
+        _require_cuda(t, what, "add_rmsnorm")
+    if x.dtype != torch.float16 or not x.is_contiguous():
+        _invalid("add_rmsnorm: x must be contiguous Float16")
+    n = x.shape[-1]
+    rows = x.numel() // n
+    out = torch.empty_like(x)
+    _check(_L.mq_add_rmsnorm_f16(_ptr(x), _ptr(delta), _ptr(weight), _ptr(out), rows, n, float(eps),
+                                 _stream_handle(x.device)))
+    return out
+
+
+def rope_kv(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, pos: torch.Tensor, k_cache: torch.Tensor,
+            v_cache: torch.Tensor, heads: int, kv_heads: int, head_dim: int) -> torch.Tensor:
+    """Rotary embedding of q and k from a fused qkv row; writes k and v into
+    the caches ``[kv_heads, max_len, head_dim]`` at device position ``pos``;
+    returns rotated q ``[heads, head_dim]``."""
+    q = torch.empty((heads, head_dim), dtype=torch.float16, device=qkv.device)
+    _check(_L.mq_rope_kv_f16(_ptr(qkv), _ptr(cos), _ptr(sin), _ptr(pos), _ptr(q), _ptr(k_cache), _ptr(v_cache),
+                             heads, kv_heads, head_dim, k_cache.shape[1], _stream_handle(qkv.device)))
+    return q
+
+
+def attention_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, pos: torch.Tensor,
+                     scale: float) -> torch.Tensor:
+    """One-token grouped-query attention over cache positions ``<= pos``;
+    returns fp16 ``[1, heads * head_dim]``."""
+    heads, head_dim = q.shape
+    L = k_cache.shape[1]
+    out = torch.empty((1, heads * head_dim), dtype=torch.float16, device=q.device)
+    wsb = _L.mq_attention_decode_workspace_size(heads, head_dim, L)
+    ws = torch.empty(max(wsb, 4), dtype=torch.uint8, device=q.device)
+    _check(_L.mq_attention_decode_f16(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(pos), _ptr(out), heads,
+                                      k_cache.shape[0], head_dim, L, float(scale), _ptr(ws), wsb,
+                                      _stream_handle(q.device)))
+    return out
+
+
 def synchronize() -> None:
     """``_C.synchronize``: wait for all queued GPU work."""
     torch.cuda.synchronize()
