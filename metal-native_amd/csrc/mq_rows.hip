@@ -58,7 +58,7 @@ constexpr int kD = MQ_ROWS_KD;     // ring depth (units in flight per wave)
 constexpr int kNW = MQ_ROWS_NW;  // wavefronts per workgroup
 constexpr int kPre = MQ_ROWS_KPRE;  // ring slots issued before the staging data is waited for
 constexpr int kXB = 8;           // activation pieces per thread per staging batch
-constexpr int kSB = 4;           // scale entries per thread per staging batch
+constexpr int kSB = 2;           // scale/zero pieces per thread per staging batch
 constexpr size_t kLds = 163840;  // LDS per CU on gfx950
 
 struct RowsKArgs {
@@ -75,7 +75,7 @@ struct RowsKArgs {
   int szrows;     // weight rows whose scales are staged (R, or 2R for SwiGLU)
   uint32_t off_sz, off_scr, off_slot;  // LDS byte offsets
   uint32_t a_bytes, sz_bytes, z_bytes;
-  uint64_t ppr_magic, g_magic;  // ceil(2^32 / d): idx / d = (idx * magic) >> 32 for the staged index ranges
+  uint64_t ppr_magic;  // ceil(2^32 / ppr): idx / ppr = (idx * magic) >> 32 for the staged index range
 };
 
 template <int FMT, int EPI, int RPW>
@@ -187,46 +187,80 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
       }
     }
   };
-  // scales/zeros of the workgroup's rows, [szrows][G] as s | z << 16
+  // scales/zeros of the workgroup's rows, [szrows][G] as s | z << 16.  The
+  // rows are one contiguous run of the [N][G] arrays (two for SwiGLU: gate
+  // and up rows), fetched as 16-byte pieces of 8 entries aligned to the
+  // array start; entries outside the run are dropped on the LDS write.
   const rsrc_t sr = make_rsrc(p.scales, p.sz_bytes);
   const rsrc_t zr = make_rsrc(p.zeros, p.z_bytes);
   const int G = p.G;
-  const int nsz = FMT != FMT_F16 ? p.szrows * G : 0;
-  const int nsb = min(kSB, (nsz + NT - 1) / NT);
-  auto s_fetch = [&](int base, uint16_t* sv, uint16_t* zv, int cnt) {
+  const uint32_t sz_real = (uint32_t)p.N * (uint32_t)G * 2u;  // bytes of the scale array
+  const int run = valid * G;                                  // entries per run
+  const int eb0 = row0 * G;                                   // first entry of run 0
+  const int eb1 = (EPI == EPI_SWIGLU ? p.F + row0 : 0) * G;   // first entry of run 1
+  const int pb0 = eb0 >> 3, np0 = run > 0 ? ((eb0 + run + 7) >> 3) - pb0 : 0;
+  const int pb1 = eb1 >> 3, np1 = (EPI == EPI_SWIGLU && run > 0) ? ((eb1 + run + 7) >> 3) - pb1 : 0;
+  const int nps = FMT != FMT_F16 ? np0 + np1 : 0;
+  const int nsb = min(kSB, (nps + NT - 1) / NT);
+  auto s_piece = [&](int idx) -> int { return idx < np0 ? pb0 + idx : pb1 + (idx - np0); };
+  auto s_fetch = [&](int base, u4* sv, u4* zv, int cnt) {
 #pragma unroll
     for (int e = 0; e < kSB; ++e) {
       if (e < cnt) {
         const int idx = base + tid + e * NT;
-        const int lr = (int)(((uint64_t)(uint32_t)idx * p.g_magic) >> 32), g = idx - lr * G;
-        int grow;
-        bool ok;
-        if (EPI == EPI_SWIGLU) {
-          const int c = lr < p.R ? lr : lr - p.R;
-          ok = c < valid;
-          grow = lr < p.R ? row0 + c : p.F + row0 + c;
-        } else {
-          ok = lr < valid;
-          grow = row0 + lr;
+        const uint32_t off = idx < nps ? (uint32_t)s_piece(idx) * 16u : kOob;
+        if (off == kOob || off + 16u <= sz_real) {
+          sv[e] = bload16(sr, off);
+          zv[e] = bload16(zr, off);
+        } else {  // the piece that straddles the end of the arrays: entry by entry
+          uint32_t sw[4], zw[4];
+#pragma unroll
+          for (int h = 0; h < 4; ++h) {
+            const uint32_t o0 = off + 4u * h, o1 = o0 + 2u;
+            const uint32_t q0 = o0 < sz_real ? o0 : kOob, q1 = o1 < sz_real ? o1 : kOob;
+            sw[h] = bload2(sr, q0) | (bload2(sr, q1) << 16);
+            zw[h] = bload2(zr, q0) | (bload2(zr, q1) << 16);
+          }
+          sv[e] = (u4){sw[0], sw[1], sw[2], sw[3]};
+          zv[e] = (u4){zw[0], zw[1], zw[2], zw[3]};
         }
-        const uint32_t off = (ok && idx < nsz) ? (uint32_t)((grow * G + g) * 2) : kOob;
-        sv[e] = bload2h(sr, off);
-        zv[e] = bload2h(zr, off);
       }
     }
   };
-  auto s_put = [&](int base, const uint16_t* sv, const uint16_t* zv, int cnt) {
+  auto s_put = [&](int base, const u4* sv, const u4* zv, int cnt) {
 #pragma unroll
     for (int e = 0; e < kSB; ++e) {
       const int idx = base + tid + e * NT;
-      if (e < cnt && idx < nsz) szl[idx] = (uint32_t)sv[e] | ((uint32_t)zv[e] << 16);
+      if (e < cnt && idx < nps) {
+        const bool second = idx >= np0;
+        const int eb = second ? eb1 : eb0;
+        const int d0 = second ? p.R * G : 0;   // LDS row block of run 1
+        const int ge = s_piece(idx) * 8;
+        const uint32_t sw[4] = {sv[e].x, sv[e].y, sv[e].z, sv[e].w};
+        const uint32_t zw[4] = {zv[e].x, zv[e].y, zv[e].z, zv[e].w};
+#pragma unroll
+        for (int h = 0; h < 8; ++h) {
+          const int le = ge + h - eb;
+          if (le >= 0 && le < run)
+            szl[d0 + le] = (h & 1) ? __builtin_amdgcn_perm(zw[h >> 1], sw[h >> 1], 0x07060302u)
+                                   : __builtin_amdgcn_perm(zw[h >> 1], sw[h >> 1], 0x05040100u);
+        }
+      }
     }
   };
+  // rows past the valid ones (last workgroup) hold zero scales
+  if (FMT != FMT_F16 && valid < p.R) {
+    const int pad = (p.R - valid) * G, nrun = EPI == EPI_SWIGLU ? 2 : 1;
+    for (int i = tid; i < nrun * pad; i += NT) {
+      const int rr = i / pad;
+      szl[rr * p.R * G + run + (i - rr * pad)] = 0u;
+    }
+  }
 
   u4 raw[kD];
   {
     u4 xv[kXB];
-    uint16_t sv[kSB], zv[kSB];
+    u4 sv[kSB], zv[kSB];
     x_fetch(0, xv, nxb);
     if (FMT != FMT_F16) s_fetch(0, sv, zv, nsb);
     // every wave's staging loads reach the texture unit first (a plain
@@ -255,8 +289,8 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
     x_fetch(base, xv, kXB);
     x_put(base, xv, kXB);
   }
-  for (int base = kSB * NT; base < nsz; base += kSB * NT) {
-    uint16_t sv[kSB], zv[kSB];
+  for (int base = kSB * NT; base < nps; base += kSB * NT) {
+    u4 sv[kSB], zv[kSB];
     s_fetch(base, sv, zv, kSB);
     s_put(base, sv, zv, kSB);
   }
@@ -509,7 +543,6 @@ hipError_t rows_launch(const LinearArgs& a, const RowsPlan& pl, hipStream_t s) {
   {
     const uint64_t ppr = (uint64_t)pl.KS * (4 * kpl_of(a.fmt) * (16 / pl.rpw)) / 8;
     k.ppr_magic = ((1ull << 32) + ppr - 1) / ppr;
-    k.g_magic = ((1ull << 32) + (uint64_t)a.G - 1) / (uint64_t)a.G;  // 2^32 for G == 1
   }
   switch (a.fmt) {
     case FMT_INT4: return launch1<FMT_INT4>(k, pl, a.epi, s);
