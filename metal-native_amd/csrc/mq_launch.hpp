@@ -49,7 +49,7 @@ hipError_t gemv_launch(const LinearArgs& a, const GemvPlan& p, void* ws, hipStre
 
 // Persistent row-block GEMV (decode with the activations resident in LDS).
 struct RowsPlan {
-  int rpw, nw, nwg, R, TW, KS, XS, maxT, szrows;
+  int rpw, nw, nwg, R, TW, KS, XS, maxT, szrows, szpad;
   uint32_t off_sz, off_scr, off_slot;
   size_t lds_bytes;
   bool ok;

@@ -73,6 +73,7 @@ struct RowsKArgs {
   int XS;         // LDS activation row stride (halves)
   int maxT;       // partial slots per wave
   int szrows;     // weight rows whose scales are staged (R, or 2R for SwiGLU)
+  int szpad;      // zero entries after them
   uint32_t off_sz, off_scr, off_slot;  // LDS byte offsets
   uint32_t a_bytes, sz_bytes, z_bytes;
   uint64_t ppr_magic;  // ceil(2^32 / ppr): idx / ppr = (idx * magic) >> 32 for the staged index range
@@ -144,17 +145,27 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
   const int nu = ((w + 1) * U) / NW - u0;
   int lt = u0 / KS, lj = u0 - lt * KS;   // load cursor (tile, step)
   int left = nu;                          // units the load cursor has not issued
-  uint32_t lro = row_off(lt);             // lane's row offset in tile lt
-  int lk = lj * KSTEP + klane;            // lane's k at the load cursor
+  // Load offset = lane part (row of tile lt + the lane's k) + step part
+  // (uniform: the buffer instruction's scalar offset).  Quantized rows are
+  // read past K without a check: the staged activations there are zero and
+  // every dequantized weight is finite, so those products vanish (past the
+  // workgroup's last row the buffer range returns zeros).  Out-of-range
+  // parts use kOobPart, so a sum of two still fails the range check.
+  constexpr uint32_t kOobPart = 0x40000000u;
+  auto lane_off = [&](int t) -> uint32_t {
+    const uint32_t ro = row_off(t);
+    return ro == kOob ? kOobPart : ro + (uint32_t)(klane * BPK2 / 2);
+  };
+  uint32_t lvo = lane_off(lt);
   auto wload = [&]() -> u4 {
-    uint32_t off = kOob;
+    uint32_t so = kOobPart, vo = lvo;
     if (left > 0) {
-      if (lk < p.K && lro != kOob) off = lro + (uint32_t)(lk * BPK2 / 2);
+      so = (uint32_t)(lj * (KSTEP * BPK2 / 2));
+      if (FMT == FMT_F16 && lj * KSTEP + klane >= p.K) vo = kOobPart;  // raw fp16 past K may hold any bits
       --left;
-      lk += KSTEP;
-      if (++lj == KS) { lj = 0; ++lt; lk = klane; lro = row_off(lt); }
+      if (++lj == KS) { lj = 0; ++lt; lvo = lane_off(lt); }
     }
-    return bload16_nt(wr, off);
+    return __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(wr, vo, so, 2));
   };
 
   // ---- staging loads, issued before the ring: the load counter completes
@@ -170,7 +181,7 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
     for (int e = 0; e < kXB; ++e) {
       if (e < cnt) {
         const int idx = base + tid + e * NT;
-        const int i = (int)(((uint64_t)(uint32_t)idx * p.ppr_magic) >> 32), c = idx - i * ppr;
+        const int i = M == 1 ? 0 : (int)(((uint64_t)(uint32_t)idx * p.ppr_magic) >> 32), c = idx - i * ppr;
         v[e] = bload16(ar, (idx < npieces && 8 * c < p.K) ? (uint32_t)((i * p.lda + 8 * c) * 2) : kOob);
       }
     }
@@ -180,7 +191,7 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
     for (int e = 0; e < kXB; ++e) {
       const int idx = base + tid + e * NT;
       if (e < cnt && idx < npieces) {
-        const int i = (int)(((uint64_t)(uint32_t)idx * p.ppr_magic) >> 32), c = idx - i * ppr;
+        const int i = M == 1 ? 0 : (int)(((uint64_t)(uint32_t)idx * p.ppr_magic) >> 32), c = idx - i * ppr;
         u4 vv = v[e];
         if (FMT == FMT_INT4) vv = perm8_int4(vv);
         *(u4*)(xs + i * p.XS + xswz(8 * c)) = vv;
@@ -248,6 +259,9 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
       }
     }
   };
+  // the tail past the last staged row, read by steps past K, holds zeros
+  if (FMT != FMT_F16)
+    for (int i = tid; i < p.szpad; i += NT) szl[p.szrows * G + i] = 0u;
   // rows past the valid ones (last workgroup) hold zero scales
   if (FMT != FMT_F16 && valid < p.R) {
     const int pad = (p.R - valid) * G, nrun = EPI == EPI_SWIGLU ? 2 : 1;
@@ -306,9 +320,13 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
 
   int ct = u0 / KS, cj = u0 - ct * KS;   // consume cursor (tile, step)
   const int ft = ct;                      // first tile of this wave
-  int ck = cj * KSTEP + klane;            // lane's k at the consume cursor
-  int szb = sz_row(ct) * G;               // lane's scale row in LDS
-  const _Float16* xa = xs + xrow + xswz(ck);
+  // scale entry of the lane's row and group: the step advances it by a
+  // uniform KSTEP / g groups (k past K reads the zero-filled tail entries or
+  // the next row's: any finite scale, the weights there meet zero activations)
+  const int sadv = p.gshift >= 31 ? 0 : (KSTEP >> p.gshift);
+  const int sl = p.gshift >= 31 ? 0 : (klane >> p.gshift);
+  int sa = sz_row(ct) * G + sl + cj * sadv;
+  const _Float16* xa = xs + xrow + xswz(cj * KSTEP + klane);
   static_assert(KSTEP % 128 == 0, "the LDS activation padding advances by a constant per unit");
   constexpr int XADV = KSTEP + (KSTEP >> 7) * 8;
   f4 acc = (f4){0.f, 0.f, 0.f, 0.f};
@@ -332,8 +350,7 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
   auto step = [&](const u4 v) {
     h2 s2 = (h2){(_Float16)0.f, (_Float16)0.f}, z2 = s2;
     if (FMT != FMT_F16) {
-      const int g = min(ck >> p.gshift, G - 1);  // k past K: zero weights, any finite scale
-      const uint32_t e = szl[szb + g];
+      const uint32_t e = szl[sa];
       s2 = as_h2(__builtin_amdgcn_perm(e, e, 0x01000100u));
       z2 = as_h2(__builtin_amdgcn_perm(e, e, 0x03020302u));
     }
@@ -363,17 +380,16 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
     for (int d = 0; d < kD; ++d) {
       if (base + d < nu) {
         step(raw[d]);
-        ck += KSTEP;
         xa += XADV;
+        sa += sadv;
         const bool last = base + d == nu - 1;
         if (++cj == KS || last) {
           flush();
           if (cj == KS) {
             cj = 0;
             ++ct;
-            ck = klane;
             xa = xs + xrow + xswz(klane);
-            szb = sz_row(ct) * G;
+            sa = sz_row(ct) * G + sl;
           }
         }
       }
@@ -504,7 +520,10 @@ RowsPlan rows_plan(const LinearArgs& a, int num_cus) {
   size_t off = al16((size_t)a.M * XS * 2);
   const int szrows = a.epi == EPI_SWIGLU ? 2 * R : R;
   p.off_sz = (uint32_t)off;
-  off += quant ? al16((size_t)szrows * a.G * 4) : 0;
+  // steps past K read up to kstep / g entries beyond a row's last group
+  const int szpad = quant && a.G != 1 ? kstep / a.g + 1 : 0;
+  if (quant && a.G != 1 && kstep % a.g != 0) return p;   // the scale entry advances by whole groups per step
+  off += quant ? al16(((size_t)szrows * a.G + szpad) * 4) : 0;
   p.off_scr = (uint32_t)off;
   off += (size_t)nw * 256 * 4;
   p.off_slot = (uint32_t)off;
@@ -520,6 +539,7 @@ RowsPlan rows_plan(const LinearArgs& a, int num_cus) {
   }
   p.rpw = rpw; p.nw = nw; p.nwg = nwg; p.R = R; p.TW = TW; p.KS = KS; p.XS = XS; p.maxT = maxT;
   p.szrows = szrows;
+  p.szpad = szpad;
   p.lds_bytes = off;
   p.ok = true;
   return p;
@@ -535,7 +555,7 @@ hipError_t rows_launch(const LinearArgs& a, const RowsPlan& pl, hipStream_t s) {
   k.C = (_Float16*)a.C; k.ldc = a.ldc;
   k.M = a.M; k.K = a.K; k.N = a.N; k.F = a.F; k.G = a.G;
   k.gshift = gshift_of(a);
-  k.R = pl.R; k.TW = pl.TW; k.KS = pl.KS; k.XS = pl.XS; k.maxT = pl.maxT; k.szrows = pl.szrows;
+  k.R = pl.R; k.TW = pl.TW; k.KS = pl.KS; k.XS = pl.XS; k.maxT = pl.maxT; k.szrows = pl.szrows; k.szpad = pl.szpad;
   k.off_sz = pl.off_sz; k.off_scr = pl.off_scr; k.off_slot = pl.off_slot;
   k.a_bytes = (uint32_t)(((int64_t)(a.M - 1) * a.lda + a.K) * 2);
   k.sz_bytes = a.fmt == FMT_F16 ? 0u : (uint32_t)(((int64_t)a.N * a.G * 2 + 3) & ~(int64_t)3);
