@@ -146,11 +146,9 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
   int lt = u0 / KS, lj = u0 - lt * KS;   // load cursor (tile, step)
   int left = nu;                          // units the load cursor has not issued
   // Load offset = lane part (row of tile lt + the lane's k) + step part
-  // (uniform: the buffer instruction's scalar offset).  Quantized rows are
-  // read past K without a check: the staged activations there are zero and
-  // every dequantized weight is finite, so those products vanish (past the
-  // workgroup's last row the buffer range returns zeros).  Out-of-range
-  // parts use kOobPart, so a sum of two still fails the range check.
+  // (uniform: the buffer instruction's scalar offset).  Only the last step
+  // checks k against K per lane.  Out-of-range parts use kOobPart, so a sum
+  // of two still fails the range check.
   constexpr uint32_t kOobPart = 0x40000000u;
   auto lane_off = [&](int t) -> uint32_t {
     const uint32_t ro = row_off(t);
@@ -161,7 +159,9 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
     uint32_t so = kOobPart, vo = lvo;
     if (left > 0) {
       so = (uint32_t)(lj * (KSTEP * BPK2 / 2));
-      if (FMT == FMT_F16 && lj * KSTEP + klane >= p.K) vo = kOobPart;  // raw fp16 past K may hold any bits
+      // the last step: no bytes past K (raw fp16 there may hold any bits, and
+      // quantized bytes there are wasted traffic)
+      if (lj == KS - 1 && lj * KSTEP + klane >= p.K) vo = kOobPart;
       --left;
       if (++lj == KS) { lj = 0; ++lt; lvo = lane_off(lt); }
     }
