@@ -136,6 +136,7 @@ SMALL = [
     (1, 128, 64, 32), (1, 896, 4864, 64), (2, 256, 100, 64), (3, 512, 130, 128), (4, 1024, 64, 128),
     (7, 384, 200, 32), (8, 2048, 192, 128), (9, 256, 64, 64), (16, 512, 96, 32), (17, 640, 128, 128),
     (33, 256, 72, 64), (64, 1024, 256, 128), (65, 256, 136, 32), (128, 512, 256, 64), (200, 384, 320, 128),
+    (129, 256, 128, 128), (300, 1024, 520, 64), (640, 2048, 384, 128),
 ]
 
 
