@@ -80,6 +80,20 @@ MQ_API int mq_dequantize(const void* weights_packed, int64_t ldw_bytes, const vo
                          const void* zeros, void* out, int64_t ldo, int64_t N, int64_t K,
                          int32_t group_size, int32_t quant_type, int32_t flat_groups, void* stream);
 
+/* Group quantizer, the inverse of the dequant formula (no reference
+ * counterpart: the reference has no quantizer and its tests pack weights by
+ * hand, tests/cpp/test_dequant_matmul.mm:104-116).  w fp16 [N, K] (row stride
+ * ldw elements, 4-byte aligned) -> weights_packed int4 [N, K/2] / int8 [N, K]
+ * (row stride ldo_bytes) and scales, zeros fp16 [N, ceil(K/group_size)]:
+ *   INT4 (asymmetric): s = half((max-min)/15) (1 if 0),
+ *     zp = clamp(rint(-min/s), 0, 15), q = clamp(rint(w/s)+zp, 0, 15),
+ *     zeros = half((zp-8)*s); K and group_size even.
+ *   INT8 (symmetric): s = half(max|w|/127) (1 if 0),
+ *     q = clamp(rint(w/s), -127, 127), zeros = 0.
+ * fp32 IEEE steps: bit-identical to the same steps on the host. */
+MQ_API int mq_quantize(const void* w, int64_t ldw, void* weights_packed, int64_t ldo_bytes, void* scales,
+                       void* zeros, int64_t N, int64_t K, int32_t group_size, int32_t quant_type, void* stream);
+
 /* fp16 matmul route for M <= 8: C[M,N] = A[M,K] . op(B), fp32 accumulation.
  * transpose_b != 0: B is [N, K] (nn.Linear weight, python/metal_native/nn/linear.py:47-49);
  * transpose_b == 0: B is [K, N].  Replaces matmul_vecmat

@@ -230,6 +230,30 @@ MQ_API int mq_dequantize(const void* weights_packed, int64_t ldw_bytes, const vo
   return MQ_SUCCESS;
 }
 
+MQ_API int mq_quantize(const void* w, int64_t ldw, void* weights_packed, int64_t ldo_bytes, void* scales,
+                       void* zeros, int64_t N, int64_t K, int32_t group_size, int32_t quant_type, void* stream) {
+  if (!w || !weights_packed || !scales || !zeros) return fail(MQ_INVALID_ARGUMENT, "quantize: null pointer argument");
+  if (N < 1 || K < 1 || N > INT32_MAX || K > INT32_MAX) return fail(MQ_INVALID_ARGUMENT, "quantize: bad shape");
+  if (group_size < 1) return fail(MQ_INVALID_ARGUMENT, "quantize: group_size must be positive");
+  if (quant_type != MQ_QUANT_INT4 && quant_type != MQ_QUANT_INT8)
+    return fail(MQ_INVALID_ARGUMENT, "quantize: quant_type must be INT4 or INT8");
+  if (quant_type == MQ_QUANT_INT4 && ((K & 1) || (group_size & 1)))
+    return fail(MQ_INVALID_ARGUMENT, "quantize: INT4 needs an even K and an even group_size");
+  if (ldw < K) return fail(MQ_INVALID_ARGUMENT, "quantize: ldw must be >= K");
+  if (ldo_bytes < (quant_type == MQ_QUANT_INT4 ? K / 2 : K))
+    return fail(MQ_INVALID_ARGUMENT, "quantize: output rows too short");
+  if ((uintptr_t)w & 3) return fail(MQ_INVALID_ARGUMENT, "quantize: weights must be 4-byte aligned");
+  mq::QuantizeArgs a{};
+  a.W = w; a.ldw = ldw; a.out = weights_packed; a.ldo = ldo_bytes;
+  a.scales = scales; a.zeros = zeros;
+  a.N = (int)N; a.K = (int)K; a.g = group_size;
+  a.G = (int)((K + group_size - 1) / group_size);
+  a.fmt = quant_type == MQ_QUANT_INT4 ? mq::FMT_INT4 : mq::FMT_INT8;
+  hipError_t e = mq::quantize_launch(a, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "quantize: kernel launch failed");
+  return MQ_SUCCESS;
+}
+
 MQ_API int mq_vecmat_f16(const void* a, int64_t lda, const void* b, int64_t ldb, void* c, int64_t ldc,
                          int64_t M, int64_t N, int64_t K, int32_t transpose_b, void* stream) {
   if (!a || !b || !c) return fail(MQ_INVALID_ARGUMENT, "matmul: null pointer argument");

@@ -80,6 +80,17 @@ struct DequantArgs {
 };
 hipError_t dequantize_launch(const DequantArgs& a, hipStream_t s);
 
+// Group quantizer (the inverse of the dequant formula): W fp16 [N, K] (row
+// stride ldw elements) -> out int4 [N, K/2] / int8 [N, K] (row stride ldo
+// bytes), scales and zeros fp16 [N, G] contiguous.
+struct QuantizeArgs {
+  const void* W; int64_t ldw;
+  void* out; int64_t ldo;
+  void* scales; void* zeros;
+  int N, K, g, G, fmt;
+};
+hipError_t quantize_launch(const QuantizeArgs& a, hipStream_t s);
+
 // Decoder glue (synthetic decode step).
 hipError_t add_rmsnorm_launch(void* x, const void* delta, const void* w, void* out, int rows, int n, float eps,
                               hipStream_t s);

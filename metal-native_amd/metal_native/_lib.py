@@ -39,6 +39,8 @@ SIGNATURES = {
                                  _i64, _i64, _i64, _i64, _i32, _i32, _i32, _c_void_p, _c_void_p]),
     "mq_dequantize": (_i32, [_c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64,
                              _i32, _i32, _i32, _c_void_p]),
+    "mq_quantize": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _c_void_p, _i64, _i64, _i32, _i32,
+                           _c_void_p]),
     "mq_vecmat_f16": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _i64, _i64, _i64, _i64,
                              _i32, _c_void_p]),
     "mq_swiglu_f16": (_i32, [_c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p]),

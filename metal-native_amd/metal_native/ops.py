@@ -238,47 +238,44 @@ def dequantize(weights_packed: torch.Tensor, scales: torch.Tensor, zeros: torch.
 # ---------------------------------------------------------------------------
 
 def quantize(w: torch.Tensor, group_size: int, quant_type: str):
-    """Quantize fp16 ``W [N, K]`` into ``(weights_packed, scales, zeros)`` of the
-    reference's storage format; the exact inverse of the dequant formula on
-    weights that lie on the quantization grid.
+    """Quantize fp16 ``W [N, K]`` (GPU tensor) into ``(weights_packed, scales,
+    zeros)`` of the reference's storage format; the exact inverse of the
+    dequant formula on weights that lie on the quantization grid.
 
-    int4 (asymmetric, per group): ``s = (max-min)/15``,
-    ``zp = clamp(round(-min/s), 0, 15)``, ``q = clamp(round(w/s)+zp, 0, 15)``,
+    int4 (asymmetric, per group): ``s = half((max-min)/15)``,
+    ``zp = clamp(rint(-min/s), 0, 15)``, ``q = clamp(rint(w/s)+zp, 0, 15)``,
     ``zeros = half((zp-8)*s)``, so ``(q-8)*s - zeros ~= (q-zp)*s``.
-    int8 (symmetric, per group): ``s = max|w|/127``, ``q = clamp(round(w/s), -127, 127)``,
-    ``zeros = 0``.
-    Runs as torch ops on ``w``'s device (an offline weight-preparation step).
+    int8 (symmetric, per group): ``s = half(max|w|/127)``,
+    ``q = clamp(rint(w/s), -127, 127)``, ``zeros = 0``.
+    Runs the library's quantize kernel (``mq_quantize``).
     """
+    op = "quantize"
+    _require_cuda(w, "weights", op)
     if w.dim() != 2:
         _invalid("quantize: weights must be 2D [N, K]")
+    if w.dtype != torch.float16:
+        _invalid("quantize: weights must be Float16")
     N, K = w.shape
     qt = quant_type_code(quant_type)
-    if qt == _lib.QUANT_INT4 and K % 2:
-        _invalid("quantize: INT4 needs an even K")
-    g = group_size
-    G = (K + g - 1) // g
-    wf = w.to(torch.float16).to(torch.float32)
-    pad = G * g - K
-    if pad:
-        wf = torch.cat([wf, wf[:, -1:].expand(N, pad)], dim=1)
-    wp = wf.reshape(N, G, g)
-    if qt == _lib.QUANT_INT4:
-        lo = wp.amin(dim=2)
-        hi = wp.amax(dim=2)
-        s = ((hi - lo) / 15.0).to(torch.float16)
-        s = torch.where(s == 0, torch.ones_like(s), s)
-        sf = s.to(torch.float32)
-        zp = torch.clamp(torch.round(-lo / sf), 0, 15)
-        q = torch.clamp(torch.round(wp / sf[:, :, None]) + zp[:, :, None], 0, 15).to(torch.uint8)
-        q = q.reshape(N, G * g)[:, :K]
-        packed = (q[:, 0::2] | (q[:, 1::2] << 4)).contiguous()
-        zeros = ((zp - 8.0) * sf).to(torch.float16)
-        return packed, s, zeros
-    amax = wp.abs().amax(dim=2)
-    s = (amax / 127.0).to(torch.float16)
-    s = torch.where(s == 0, torch.ones_like(s), s)
-    q = torch.clamp(torch.round(wp / s.to(torch.float32)[:, :, None]), -127, 127).to(torch.int8)
-    return q.reshape(N, G * g)[:, :K].contiguous(), s, torch.zeros_like(s)
+    if qt == _lib.QUANT_INT4 and (K % 2 or group_size % 2):
+        _invalid("quantize: INT4 needs an even K and an even group_size")
+    if group_size < 1:
+        _invalid("quantize: group_size must be positive")
+    if w.stride(-1) != 1 or w.data_ptr() % 4:
+        w = w.contiguous()
+    G = (K + group_size - 1) // group_size
+    dev = w.device
+    cols = K // 2 if qt == _lib.QUANT_INT4 else K
+    packed = torch.empty((N, cols), dtype=torch.uint8 if qt == _lib.QUANT_INT4 else torch.int8, device=dev)
+    scales = torch.empty((N, G), dtype=torch.float16, device=dev)
+    zeros = torch.empty((N, G), dtype=torch.float16, device=dev)
+    if N == 0 or K == 0:
+        return packed, scales, zeros
+    with torch.cuda.device(dev):
+        rc = _L.mq_quantize(_ptr(w), w.stride(0), _ptr(packed), cols, _ptr(scales), _ptr(zeros), N, K,
+                            group_size, qt, _stream_handle(dev))
+    _check(rc)
+    return packed, scales, zeros
 
 
 # ---------------------------------------------------------------------------

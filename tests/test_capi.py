@@ -26,7 +26,8 @@ def lib():
 
 def test_header_declares_entry_points():
     names = declared()
-    for want in ["mq_dequant_matmul", "mq_dequantize", "mq_vecmat_f16", "mq_swiglu_f16", "mq_last_error"]:
+    for want in ["mq_dequant_matmul", "mq_dequantize", "mq_quantize", "mq_vecmat_f16", "mq_swiglu_f16",
+                 "mq_last_error"]:
         assert want in names
 
 
@@ -101,19 +102,11 @@ def test_python_rejects_cpu_tensors():
                           torch.zeros(8, 2, dtype=torch.float16), 32, "int4")
 
 
-def test_quantize_matches_oracle_on_cpu():
-    """quantize() is device-agnostic torch code; on CPU tensors it must agree
-    with the oracle's quantizer bit for bit."""
-    import numpy as np
+def test_quantize_needs_a_gpu_tensor():
+    """The quantizer runs on the library's kernel only: CPU tensors are refused."""
     import torch
 
     import metal_native as mn
-    from oracle import mq_oracle as O
 
-    w = (np.random.default_rng(0).standard_normal((12, 256)) * 0.1).astype(np.float16)
-    for qt in ("int4", "int8"):
-        bp, s, z = mn.quantize(torch.from_numpy(w), 64, qt)
-        obp, os_, oz = O.quantize(w, 64, qt)
-        np.testing.assert_array_equal(bp.numpy().view(np.uint8), obp.view(np.uint8))
-        np.testing.assert_array_equal(s.numpy(), os_)
-        np.testing.assert_array_equal(z.numpy(), oz)
+    with pytest.raises(mn.MetalNativeError, match="GPU tensor"):
+        mn.quantize(torch.zeros(4, 64, dtype=torch.float16), 32, "int4")

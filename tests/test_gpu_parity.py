@@ -464,3 +464,37 @@ def test_decode_variants(mn, gpu, opts, M, K, N, g, qt, epi):
         check_close(y, acc + b.astype(np.float32), f"decode bias {opts}")
     else:
         check_close(y, acc, f"decode {opts}")
+
+
+# ---------------------------------------------------------------------------
+# quantize kernel: bit-exact against the oracle's quantizer
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("qt", ["int4", "int8"])
+@pytest.mark.parametrize("N,K,g", [(12, 256, 64), (7, 200, 32), (33, 1000, 128), (64, 896, 64), (5, 130, 128),
+                                   (3584, 18944, 128), (16, 3584, 3584)])
+def test_quantize_bit_exact(mn, gpu, qt, N, K, g):
+    say(f"quantize {qt} N={N} K={K} g={g}")
+    rng = np.random.default_rng(N + K + g)
+    w = (rng.standard_normal((N, K)) * rng.uniform(0.01, 0.3, size=(N, 1))).astype(np.float16)
+    w[0, : min(K, g)] = 0          # an all-zero group (scale 1)
+    if N > 1:
+        w[1, :4] = np.float16(6e-8)  # fp16 subnormals
+    bp, s, z = mn.quantize(dev(w, gpu), g, qt)
+    obp, os_, oz = O.quantize(w, g, qt)
+    np.testing.assert_array_equal(host(bp).view(np.uint8), obp.view(np.uint8))
+    np.testing.assert_array_equal(host(s).view(np.uint16), os_.view(np.uint16))
+    np.testing.assert_array_equal(host(z).view(np.uint16), oz.view(np.uint16))
+    # and the kernels consume what it produced: dequantize matches the oracle's dequant of it
+    W = mn.dequantize(bp, s, z, g, qt, K=K)
+    np.testing.assert_array_equal(host(W).view(np.uint16), O.dequantize(obp, os_, oz, K, g, qt).view(np.uint16))
+
+
+def test_quantize_strided_input(mn, gpu):
+    say("quantize strided")
+    w = (np.random.default_rng(3).standard_normal((8, 512)) * 0.05).astype(np.float16)
+    big = dev(np.concatenate([w, np.zeros((8, 64), np.float16)], axis=1), gpu)
+    bp, s, z = mn.quantize(big[:, :512], 128, "int4")
+    obp, os_, oz = O.quantize(w, 128, "int4")
+    np.testing.assert_array_equal(host(bp).view(np.uint8), obp.view(np.uint8))
+    np.testing.assert_array_equal(host(s).view(np.uint16), os_.view(np.uint16))
