@@ -15,6 +15,9 @@ import types
 from .ops import (MetalNativeError, dequant_matmul, dequantize, last_path, matmul, quantize,
                   set_option, swiglu, synchronize)
 
+from . import nn, qformat  # noqa: E402  (layers, on-disk format and converters)
+from .qcache import QuantWeightCache  # noqa: E402
+
 fast = types.SimpleNamespace(swiglu=swiglu)
 
 # reference-style `_C` namespace (bindings/bind_core.cpp:102)
@@ -27,4 +30,4 @@ _C = types.SimpleNamespace(
 )
 
 __all__ = ["MetalNativeError", "dequant_matmul", "dequantize", "quantize", "matmul", "swiglu",
-           "fast", "synchronize", "set_option", "last_path", "_C"]
+           "fast", "synchronize", "set_option", "last_path", "_C", "nn", "qformat", "QuantWeightCache"]

@@ -287,3 +287,55 @@ def make_int8_problem(M: int, K: int, N: int, seed: int = 0, g: int | None = Non
     z = np.zeros_like(s)
     x = rng.standard_normal((M, K), dtype=np.float32).astype(np.float16)
     return x, q, s, z, gg
+
+
+# --------------------------------------------------------------------------
+# GPTQ / AWQ checkpoints -> the reference's storage format
+# --------------------------------------------------------------------------
+# Neither format appears in the reference; they are the two common 4-bit
+# checkpoint layouts (AutoGPTQ's original "gptq" format and AutoAWQ's GEMM
+# format), restated from their published packing rules:
+#   GPTQ: qweight int32 [K/8, N], word (i, n) holds q[n, 8i + j] at bits 4j;
+#         qzeros int32 [G, N/8], word (g, c) holds zp[g, 8c + j] - 1 at bits 4j;
+#         scales fp16 [G, N]; w = (q - zp) * s.
+#   AWQ:  qweight int32 [K, N/8], word (k, c) holds q[8c + ORDER[j], k] at bits 4j
+#         with ORDER = (0, 2, 4, 6, 1, 3, 5, 7); qzeros int32 [G, N/8] likewise
+#         (no offset); scales fp16 [G, N]; w = (q - zp) * s.
+# The reference form keeps q and sets zeros = half((zp - 8) * s).
+
+AWQ_ORDER = (0, 2, 4, 6, 1, 3, 5, 7)
+
+
+def _words_to_nibbles(words: np.ndarray) -> np.ndarray:
+    u = np.asarray(words).astype(np.int64) & 0xFFFFFFFF
+    return np.stack([(u >> (4 * j)) & 0xF for j in range(8)], axis=-1).astype(np.uint8)
+
+
+def gptq_to_reference(qweight, qzeros, scales, g: int, zero_offset: int = 1):
+    """-> (Bp uint8 [N, K/2], scales fp16 [N, G], zeros fp16 [N, G])."""
+    K8, N = qweight.shape
+    K = 8 * K8
+    q = _words_to_nibbles(qweight).transpose(1, 0, 2).reshape(N, K)        # [N, K]
+    zp = _words_to_nibbles(qzeros).reshape(qzeros.shape[0], -1)[:, :N].astype(np.int32) + zero_offset
+    s = np.asarray(scales, dtype=np.float16)
+    z = ((zp.astype(np.float32) - 8.0) * s.astype(np.float32)).astype(np.float16)
+    return pack_int4(q), s.T.copy(), z.T.copy()
+
+
+def awq_to_reference(qweight, qzeros, scales, g: int):
+    K, N8 = qweight.shape
+    N = 8 * N8
+    inv = np.argsort(np.asarray(AWQ_ORDER))
+    q = _words_to_nibbles(qweight)[:, :, inv].reshape(K, N).T              # [N, K]
+    zp = _words_to_nibbles(qzeros)[:, :, inv].reshape(qzeros.shape[0], N).astype(np.int32)
+    s = np.asarray(scales, dtype=np.float16)
+    z = ((zp.astype(np.float32) - 8.0) * s.astype(np.float32)).astype(np.float16)
+    return pack_int4(np.ascontiguousarray(q)), s.T.copy(), z.T.copy()
+
+
+def dequant_zero_point(q, zp, scales, g: int) -> np.ndarray:
+    """The checkpoints' own dequant ``(q - zp) * s`` in fp32 then one fp16
+    rounding: q uint8 [N, K], zp int [N, G], scales fp16 [N, G]."""
+    K = q.shape[1]
+    return ((q.astype(np.float32) - _expand_groups(zp.astype(np.float32), K, g))
+            * _expand_groups(np.asarray(scales, np.float16).astype(np.float32), K, g)).astype(np.float16)

@@ -498,3 +498,28 @@ def test_quantize_strided_input(mn, gpu):
     obp, os_, oz = O.quantize(w, 128, "int4")
     np.testing.assert_array_equal(host(bp).view(np.uint8), obp.view(np.uint8))
     np.testing.assert_array_equal(host(s).view(np.uint16), os_.view(np.uint16))
+
+
+def test_gptq_checkpoint_through_the_kernels(mn, gpu):
+    """A GPTQ checkpoint converted on the GPU runs through dequant_matmul: the
+    conversion matches the host one and the product matches the oracle."""
+    from metal_native import qformat as QF
+
+    say("gptq conversion on gpu")
+    rng = np.random.default_rng(11)
+    N, K, g, M = 256, 1024, 128, 3
+    G = K // g
+    q = rng.integers(0, 16, size=(N, K), dtype=np.uint8)
+    zp = rng.integers(1, 17, size=(G, N))
+    s = rng.uniform(0.002, 0.03, size=(G, N)).astype(np.float16)
+    u = q.reshape(N, K // 8, 8).astype(np.uint64)
+    qw = sum(u[:, :, j] << np.uint64(4 * j) for j in range(8)).T.astype(np.uint32).view(np.int32)
+    z = (zp - 1).reshape(G, N // 8, 8).astype(np.uint64)
+    qz = sum(z[:, :, j] << np.uint64(4 * j) for j in range(8)).astype(np.uint32).view(np.int32)
+    cw = QF.from_gptq(dev(qw, gpu), dev(qz, gpu), dev(s, gpu), g)
+    bp, ss, zz = O.gptq_to_reference(qw, qz, s, g)
+    np.testing.assert_array_equal(host(cw.packed), bp)
+    np.testing.assert_array_equal(host(cw.zeros).view(np.uint16), zz.view(np.uint16))
+    x = rng.standard_normal((M, K)).astype(np.float16)
+    y = host(mn.dequant_matmul(dev(x, gpu), cw.packed, cw.scales, cw.zeros, g, "int4"))
+    check_close(y, O.matmul_f32acc(x, O.dequant_int4(bp, ss, zz, K, g)), "gptq checkpoint")
