@@ -207,6 +207,62 @@ def decode_bench(device):
     return r
 
 
+def prep_bench(device, reps: int = 50):
+    """Weight-preparation kernels at the config-2 shape (K=18944, N=3584,
+    g=128), timed in a HIP graph: ``quantize`` (fp16 W -> int4 + scales +
+    zeros; reads 2 B and writes 0.5 B per weight plus 4 B per group) and the
+    flat ``dequantize`` behind QuantWeightCache.get_dequantized (reads 0.5 B +
+    2 B per group, writes 2 B per weight)."""
+    import torch
+
+    import metal_native as mn
+
+    N, K, g = 3584, 18944, 128
+    G = K // g
+    gen = torch.Generator(device=device)
+    gen.manual_seed(0)
+    copies = 3   # 3 x 136 MB of fp16 weights exceed the 256 MB MALL
+    ws = [(torch.randn((N, K), device=device, generator=gen) * 0.05).half() for _ in range(copies)]
+    out = {}
+
+    def timed(fn):
+        stream = torch.cuda.Stream(device)
+        stream.wait_stream(torch.cuda.current_stream(device))
+        with torch.cuda.stream(stream):
+            for i in range(copies):
+                fn(i)
+        torch.cuda.synchronize(device)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            for i in range(reps):
+                fn(i % copies)
+        graph.replay()
+        torch.cuda.synchronize(device)
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        cur = torch.cuda.current_stream(device)
+        t0.record(cur)
+        graph.replay()
+        t1.record(cur)
+        torch.cuda.synchronize(device)
+        return t0.elapsed_time(t1) * 1e3 / reps
+
+    us = timed(lambda i: mn.quantize(ws[i], g, "int4"))
+    nbytes = N * K * 2 + N * K // 2 + 4 * N * G
+    out["quantize_int4_cfg2"] = {"us_per_call": round(us, 2), "algo_bytes": nbytes,
+                                 "GB/s": round(nbytes / us / 1e3, 1), "pct_hbm_peak": round(nbytes / us / 1e3 / 80, 1)}
+    qs = [mn.quantize(w, g, "int4") for w in ws]
+    flat = [(bp.reshape(1, -1), s.reshape(-1)) for bp, s, _ in qs]
+    del ws
+    us = timed(lambda i: mn.dequantize(flat[i][0], flat[i][1], None, g, "int4", K=N * K, flat_groups=True))
+    nbytes = N * K // 2 + 2 * N * G + 2 * N * K
+    out["dequantize_flat_int4_cfg2"] = {"us_per_call": round(us, 2), "algo_bytes": nbytes,
+                                        "GB/s": round(nbytes / us / 1e3, 1),
+                                        "pct_hbm_peak": round(nbytes / us / 1e3 / 80, 1)}
+    torch.cuda.empty_cache()
+    return out
+
+
 # --------------------------------------------------------------------------
 # CPU baseline: the oracle on this host
 # --------------------------------------------------------------------------
@@ -324,6 +380,11 @@ def main():
             log(f"[bench] cfg5: {json.dumps(results['cfg5_qwen7b_decode_64tok'])}")
         except Exception as e:  # noqa: BLE001  (the headline line must still print)
             results["cfg5_qwen7b_decode_64tok"] = {"error": repr(e)}
+        try:
+            log("[bench] weight preparation (quantize, flat dequantize) ...")
+            results.update(prep_bench(device))
+        except Exception as e:  # noqa: BLE001
+            results["prep"] = {"error": repr(e)}
 
     cpu = None
     if not args.no_cpu:

@@ -13,10 +13,11 @@
 // round-to-nearest-even) or an RNE conversion, so the result is bit-identical
 // to the same steps in numpy.
 //
-// One wavefront per (row, group): the group's elements are read coalesced,
-// min/max reduced across the wave, then each lane writes whole bytes (int4:
-// a lane owns k pairs, so g must be even).  HBM-bound: 2 bytes read and 0.5
-// (int4) or 1 (int8) byte written per weight.
+// General path: one wavefront per (row, group), the group's elements read
+// coalesced, min/max reduced across the wave, each lane writing whole bytes
+// (int4: a lane owns k pairs, so g must be even).  Vector path (power-of-two
+// g, aligned rows): g/8 lanes per group, 16-byte loads, 4- or 8-byte stores.
+// HBM-bound: 2 bytes read and 0.5 (int4) or 1 (int8) byte written per weight.
 #include "mq_device.hpp"
 #include "mq_launch.hpp"
 
@@ -90,10 +91,96 @@ __global__ __launch_bounds__(256) void quantize_kernel(QuantizeArgs p) {
   }
 }
 
+// Vector path (g a power of two in 8..512, K and the row stride multiples of
+// 8, 16-byte aligned rows): L = g/8 lanes per group, each lane one 16-byte
+// piece of 8 weights; a wave covers 64/L groups.  Same arithmetic as above.
+template <int FMT>
+__global__ __launch_bounds__(256) void quantize_vec_kernel(QuantizeArgs p, int lshift) {
+  const int lane = threadIdx.x & 63;
+  const int L = 1 << lshift;
+  const int64_t wave = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t item = (wave << (6 - lshift)) + (lane >> lshift);   // (row, group)
+  const bool live = item < (int64_t)p.N * p.G;
+  const int64_t it = live ? item : 0;
+  const int n = (int)(it / p.G), j = (int)(it - (int64_t)n * p.G);
+  const int k = j * p.g + (lane & (L - 1)) * 8;
+  const bool have = live && k < p.K;
+  h8 v = {};
+  if (have) v = *(const h8*)((const _Float16*)p.W + (int64_t)n * p.ldw + k);
+  float lo = INFINITY, hi = -INFINITY;
+  if (have) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float f = (float)v[e];
+      if (FMT == FMT_INT4) {
+        lo = fminf(lo, f);
+        hi = fmaxf(hi, f);
+      } else {
+        hi = fmaxf(hi, fabsf(f));
+      }
+    }
+  }
+  for (int o = 1; o < L; o <<= 1) {
+    hi = fmaxf(hi, __shfl_xor(hi, o));
+    if (FMT == FMT_INT4) lo = fminf(lo, __shfl_xor(lo, o));
+  }
+  float sf, zp = 0.f;
+  _Float16 s16, z16 = (_Float16)0.f;
+  if (FMT == FMT_INT4) {
+    s16 = (_Float16)((hi - lo) / 15.0f);
+    if (s16 == (_Float16)0.f) s16 = (_Float16)1.f;
+    sf = (float)s16;
+    zp = fminf(fmaxf(rintf(-lo / sf), 0.f), 15.f);
+    z16 = (_Float16)((zp - 8.0f) * sf);
+  } else {
+    s16 = (_Float16)(hi / 127.0f);
+    if (s16 == (_Float16)0.f) s16 = (_Float16)1.f;
+    sf = (float)s16;
+  }
+  if (live && (lane & (L - 1)) == 0) {
+    ((_Float16*)p.scales)[it] = s16;   // [N, G] contiguous: index n*G + j
+    ((_Float16*)p.zeros)[it] = z16;
+  }
+  if (!have) return;
+  if (FMT == FMT_INT4) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float q = fminf(fmaxf(rintf((float)v[e] / sf) + zp, 0.f), 15.f);
+      word |= (uint32_t)(int)q << (4 * e);
+    }
+    *(uint32_t*)((unsigned char*)p.out + (int64_t)n * p.ldo + (k >> 1)) = word;
+  } else {
+    uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int q = (int)fminf(fmaxf(rintf((float)v[e] / sf), -127.f), 127.f);
+      if (e < 4) w0 |= (uint32_t)(q & 0xFF) << (8 * e);
+      else w1 |= (uint32_t)(q & 0xFF) << (8 * (e - 4));
+    }
+    *(uint2*)((unsigned char*)p.out + (int64_t)n * p.ldo + k) = make_uint2(w0, w1);
+  }
+}
+
 }  // namespace
 
 hipError_t quantize_launch(const QuantizeArgs& a, hipStream_t s) {
   const int64_t items = (int64_t)a.N * a.G;
+  int lshift = -1;
+  for (int b = 0; b <= 6; ++b)
+    if (a.g == 8 << b) lshift = b;
+  const bool vec = lshift >= 0 && a.K % 8 == 0 && a.ldw % 8 == 0 && ((uintptr_t)a.W & 15) == 0 &&
+                   (a.fmt == FMT_INT4 ? (a.ldo % 4 == 0 && ((uintptr_t)a.out & 3) == 0)
+                                      : (a.ldo % 8 == 0 && ((uintptr_t)a.out & 7) == 0));
+  if (vec) {
+    const int64_t waves = (items + (64 >> lshift) - 1) / (64 >> lshift);
+    const dim3 grid((unsigned)((waves + 3) / 4));
+    if (a.fmt == FMT_INT4)
+      hipLaunchKernelGGL(quantize_vec_kernel<FMT_INT4>, grid, dim3(256), 0, s, a, lshift);
+    else
+      hipLaunchKernelGGL(quantize_vec_kernel<FMT_INT8>, grid, dim3(256), 0, s, a, lshift);
+    return hipGetLastError();
+  }
   const dim3 grid((unsigned)((items + 3) / 4));
   if (a.fmt == FMT_INT4)
     hipLaunchKernelGGL(quantize_kernel<FMT_INT4>, grid, dim3(256), 0, s, a);
