@@ -440,18 +440,19 @@ GemvPlan gemv_plan(const LinearArgs& a, int num_cus, const GemvTuning& tu) {
       const int64_t nwg = (int64_t)nq * P;
       if (nwg > 0x7fffffff) continue;
       // Time model (microseconds) for the most loaded CU: weight streaming at
-      // its share of ~7 TB/s, dequant VALU at 64 lane-ops per clock, one load
-      // latency per round of resident waves (16 per CU), and the split-K
-      // partial traffic.
+      // its share of ~7 TB/s or the dequant VALU at 64 lane-ops per clock,
+      // plus a fixed cost per resident wave (staging the activation window
+      // and scales, the partial store: about 0.25 us each, measured at the
+      // config-2 shapes), plus the split-K partial traffic.
       const double wg_cu = std::ceil((double)nwg / num_cus);
       const double bytes_cu = wg_cu * tpw * KKmax * step_bytes;
       const double t_mem = bytes_cu / 27.0e3;
       const double wpb = a.fmt == FMT_INT4 ? 2.0 : 1.0;                      // weights per byte
       const double ops = a.fmt == FMT_INT4 ? 2.2 : (a.fmt == FMT_INT8 ? 2.0 : 0.3);
       const double t_valu = bytes_cu * wpb * ops / (64.0 * 2400.0);
-      const double t_lat = std::ceil(wg_cu * tpw / 16.0) * 1.5;
+      const double t_wave = 0.25 * wg_cu * tpw;
       const double t_part = P > 1 ? (double)P * a.M * T * rpw * 8.0 / num_cus / 27.0e3 : 0.0;
-      const double cost = std::max(std::max(t_mem, t_valu), t_lat) + t_part;
+      const double cost = std::max(t_mem, t_valu) + t_wave + t_part;
       if (cost < best * 0.999) {
         best = cost;
         p.rpw = rpw; p.tpw = tpw; p.P = P; p.kk = KKmax; p.nq = nq; p.nwg = (int)nwg;
