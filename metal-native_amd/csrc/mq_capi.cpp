@@ -335,6 +335,28 @@ MQ_API int mq_attention_decode_f16(const void* q, const void* k_cache, const voi
   return MQ_SUCCESS;
 }
 
+MQ_API int64_t mq_attention_decode_rope_workspace_size(int32_t heads, int32_t head_dim, int64_t max_len) {
+  if (heads < 1 || max_len < 1 || !mq::attn_fused_supported(heads, head_dim, max_len)) return -1;
+  return (int64_t)mq::attn_fused_workspace(heads, head_dim, max_len);
+}
+
+MQ_API int mq_attention_decode_rope_f16(const void* qkv, const float* cos_table, const float* sin_table,
+                                        const int64_t* pos, void* k_cache, void* v_cache, void* out, int32_t heads,
+                                        int32_t kv_heads, int32_t head_dim, int64_t max_len, float scale,
+                                        void* workspace, int64_t workspace_bytes, void* stream) {
+  if (!qkv || !cos_table || !sin_table || !pos || !k_cache || !v_cache || !out || !workspace)
+    return fail(MQ_INVALID_ARGUMENT, "attention_decode_rope: null pointer argument");
+  if (heads < 1 || kv_heads < 1 || heads % kv_heads || max_len < 1 ||
+      !mq::attn_fused_supported(heads, head_dim, max_len))
+    return fail(MQ_INVALID_ARGUMENT, "attention_decode_rope: bad shape (head_dim 64 or 128, max_len <= 4096)");
+  if (workspace_bytes < (int64_t)mq::attn_fused_workspace(heads, head_dim, max_len))
+    return fail(MQ_INVALID_ARGUMENT, "attention_decode_rope: workspace too small");
+  hipError_t e = mq::attn_fused_launch(qkv, cos_table, sin_table, pos, k_cache, v_cache, out, heads, kv_heads,
+                                       head_dim, max_len, scale, workspace, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "attention_decode_rope: kernel launch failed");
+  return MQ_SUCCESS;
+}
+
 MQ_API int mq_set_option(const char* key, int64_t value) {
   if (!key) return fail(MQ_INVALID_ARGUMENT, "set_option: null key");
   if (std::strcmp(key, "force_path") == 0) {

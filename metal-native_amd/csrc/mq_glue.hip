@@ -8,6 +8,8 @@
 #include "mq_device.hpp"
 #include "mq_launch.hpp"
 
+#include <algorithm>
+
 namespace mq {
 namespace {
 
@@ -34,7 +36,43 @@ __device__ float block_reduce(float v, float* red) {
   return r;
 }
 
-// x <- half(x + delta) (if delta); out = half(x * rsqrt(mean(x^2) + eps) * w)
+// x <- half(x + delta) (if delta); out = half(x * rsqrt(mean(x^2) + eps) * w).
+// Rows of up to 8 * 1024 elements, n a multiple of 8: thread t owns elements
+// [8t, 8t + 8) in registers (one 16-byte load per array, one memory round
+// trip, one block reduction).
+__global__ __launch_bounds__(1024) void add_rmsnorm_reg_kernel(_Float16* x, const _Float16* delta, const _Float16* w,
+                                                                _Float16* out, int n, float eps) {
+  __shared__ float red[16];
+  _Float16* xr = x + (int64_t)blockIdx.x * n;
+  const _Float16* dr = delta ? delta + (int64_t)blockIdx.x * n : nullptr;
+  _Float16* orow = out + (int64_t)blockIdx.x * n;
+  const int i0 = 8 * threadIdx.x;
+  const bool have = i0 < n;
+  h8 v = {}, wv = {}, dv = {};
+  if (have) {
+    v = *(const h8*)(xr + i0);
+    wv = *(const h8*)(w + i0);
+    if (dr) dv = *(const h8*)(dr + i0);
+  }
+  float ss = 0.f;
+  if (have) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      if (dr) v[e] = (_Float16)((float)v[e] + (float)dv[e]);
+      const float f = (float)v[e];
+      ss += f * f;
+    }
+    if (dr) *(h8*)(xr + i0) = v;
+  }
+  const float r = rsqrtf(block_reduce<false>(ss, red) / (float)n + eps);
+  if (have) {
+    h8 o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = (_Float16)((float)v[e] * r * (float)wv[e]);
+    *(h8*)(orow + i0) = o;
+  }
+}
+
 __global__ __launch_bounds__(1024) void add_rmsnorm_kernel(_Float16* x, const _Float16* delta, const _Float16* w,
                                                             _Float16* out, int n, float eps) {
   __shared__ float red[16];
@@ -138,6 +176,80 @@ __global__ __launch_bounds__(64) void attn_partial_kernel(const _Float16* q, con
   if (lane == 0) { rec[0] = m; rec[1] = l; }
 }
 
+// The same with the head dimension known at compile time (64 or 128): lane
+// = position for both phases, its K and V rows loaded together up front (one
+// memory round trip); p * V goes through LDS so that lanes then sum columns
+// over the split's positions in position order.  Positions past pos read a
+// clamped row (finite values) with weight 0.
+template <int D>
+__global__ __launch_bounds__(64) void attn_partial_d_kernel(const _Float16* q, const _Float16* kc, const _Float16* vc,
+                                                             const int64_t* pos_p, float* ws, int H, int KVH,
+                                                             int64_t L, float scale) {
+  __shared__ float qs[D];
+  __shared__ float pv[kSplit * (D + 1)];
+  const int c = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
+  const int kvh = h / (H / KVH);
+  const int n = (int)(*pos_p) + 1;
+  const int t0 = c * kSplit;
+  float* rec = ws + ((int64_t)h * gridDim.x + c) * (D + 2);  // [m, l, o[D]]
+  if (t0 >= n) {
+    if (lane == 0) { rec[0] = -INFINITY; rec[1] = 0.f; }
+    for (int j = lane; j < D; j += 64) rec[2 + j] = 0.f;
+    return;
+  }
+  const int t = t0 + lane;
+  const int64_t row = ((int64_t)kvh * L + min((int64_t)t, L - 1)) * D;
+  h8 kv[D / 8], vv[D / 8];
+#pragma unroll
+  for (int j = 0; j < D / 8; ++j) kv[j] = *(const h8*)(kc + row + 8 * j);
+#pragma unroll
+  for (int j = 0; j < D / 8; ++j) vv[j] = *(const h8*)(vc + row + 8 * j);
+  for (int j = lane; j < D; j += 64) qs[j] = (float)q[h * D + j];
+  __syncthreads();
+  float acc = 0.f;
+#pragma unroll
+  for (int j = 0; j < D / 8; ++j)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc += qs[8 * j + e] * (float)kv[j][e];
+  const float s = t < n ? acc * scale : -INFINITY;
+  const float m = wave_max(s);
+  const float p = t < n ? expf(s - m) : 0.f;
+  const float l = wave_sum(p);
+#pragma unroll
+  for (int j = 0; j < D / 8; ++j)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) pv[lane * (D + 1) + 8 * j + e] = p * (float)vv[j][e];
+  __syncthreads();
+  for (int col = lane; col < D; col += 64) {
+    float o = 0.f;
+#pragma unroll 16
+    for (int u = 0; u < kSplit; ++u) o += pv[u * (D + 1) + col];
+    rec[2 + col] = o;
+  }
+  if (lane == 0) { rec[0] = m; rec[1] = l; }
+}
+
+// One wave per head: lanes hold the splits' maxima and sums (wave
+// reductions), then lane j accumulates columns j, j+64, ... over the splits.
+__global__ __launch_bounds__(64) void attn_combine_wave_kernel(const float* ws, _Float16* out, int nsplit, int D) {
+  __shared__ float wgt[64];
+  const int h = blockIdx.x, lane = threadIdx.x;
+  const float* base = ws + (int64_t)h * nsplit * (D + 2);
+  const float mc = lane < nsplit ? base[lane * (D + 2)] : -INFINITY;
+  const float lc = lane < nsplit ? base[lane * (D + 2) + 1] : 0.f;
+  const float m = wave_max(mc);
+  const float wc = mc != -INFINITY ? expf(mc - m) : 0.f;
+  const float l = wave_sum(lc * wc);
+  wgt[lane] = wc;
+  __syncthreads();
+  for (int j = lane; j < D; j += 64) {
+    float a = 0.f;
+#pragma unroll 4
+    for (int c = 0; c < nsplit; ++c) a += base[c * (D + 2) + 2 + j] * wgt[c];
+    out[h * D + j] = (_Float16)(a / l);
+  }
+}
+
 __global__ __launch_bounds__(128) void attn_combine_kernel(const float* ws, _Float16* out, int nsplit, int D) {
   const int h = blockIdx.x;
   const float* base = ws + (int64_t)h * nsplit * (D + 2);
@@ -158,10 +270,149 @@ __global__ __launch_bounds__(128) void attn_combine_kernel(const float* ws, _Flo
   }
 }
 
+// Rotary embedding + cache write + attention + split combine in one launch.
+// Workgroup (split c, head h), lane = position, as attn_partial_d_kernel, and:
+//  * q of head h is rotated here, rounded to fp16 as rope_kv stores it;
+//  * the split holding position pos rotates k and takes v of the new token
+//    from qkv and uses them for that position; the workgroup of the first
+//    query head of each KV group writes them into the caches (no other
+//    workgroup reads position pos);
+//  * the split's record (m, l, o[D]) goes out with system-scope stores (the
+//    splits of a head run on different XCDs), then a per-head counter elects
+//    the last workgroup of the head, which combines the splits in split order
+//    and resets the counter (counters start at zero, calls are stream-ordered).
+template <int D>
+__global__ __launch_bounds__(64) void attn_fused_d_kernel(const _Float16* qkv, const float* cos_t, const float* sin_t,
+                                                           const int64_t* pos_p, _Float16* kc, _Float16* vc,
+                                                           _Float16* out, float* ws, unsigned int* cnt, int H,
+                                                           int KVH, int64_t L, float scale) {
+  __shared__ float qs[D];
+  __shared__ float knew[D], vnew[D];
+  __shared__ float pv[kSplit * (D + 1)];
+  __shared__ float wgt[64];
+  __shared__ unsigned int s_arrived;
+  const int c = blockIdx.x, h = blockIdx.y, lane = threadIdx.x, nsplit = gridDim.x;
+  const int grp = H / KVH, kvh = h / grp;
+  const int64_t pos = *pos_p;
+  const int n = (int)pos + 1;
+  const int t0 = c * kSplit;
+  const float* cs = cos_t + pos * D;
+  const float* sn = sin_t + pos * D;
+  constexpr int HALF = D / 2;
+  auto rope = [&](const _Float16* src, int j) -> _Float16 {
+    const float x = (float)src[j];
+    const float pair = (float)src[j < HALF ? j + HALF : j - HALF];
+    const float rot = j < HALF ? -pair : pair;
+    return (_Float16)(x * cs[j] + rot * sn[j]);
+  };
+  float* rec = ws + ((int64_t)h * nsplit + c) * (D + 2);  // [m, l, o[D]]
+  auto put = [&](float* a, float v) { __hip_atomic_store(a, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM); };
+  if (t0 >= n) {
+    if (lane == 0) { put(rec, -INFINITY); put(rec + 1, 0.f); }
+    for (int j = lane; j < D; j += 64) put(rec + 2 + j, 0.f);
+  } else {
+    const int t = t0 + lane;
+    const bool mine = pos >= t0 && pos < t0 + kSplit;   // this split holds the new token
+    const int64_t row = ((int64_t)kvh * L + min((int64_t)t, L - 1)) * D;
+    h8 kv[D / 8], vv[D / 8];
+#pragma unroll
+    for (int j = 0; j < D / 8; ++j) kv[j] = *(const h8*)(kc + row + 8 * j);
+#pragma unroll
+    for (int j = 0; j < D / 8; ++j) vv[j] = *(const h8*)(vc + row + 8 * j);
+    const _Float16* qrow = qkv + h * D;
+    const _Float16* krow = qkv + (H + kvh) * D;
+    const _Float16* vsrc = qkv + (H + KVH + kvh) * D;
+    for (int j = lane; j < D; j += 64) qs[j] = (float)rope(qrow, j);
+    if (mine) {
+      const int64_t prow = ((int64_t)kvh * L + pos) * D;
+      for (int j = lane; j < D; j += 64) {
+        const _Float16 kn = rope(krow, j), vn = vsrc[j];
+        knew[j] = (float)kn;
+        vnew[j] = (float)vn;
+        if (h % grp == 0) {
+          kc[prow + j] = kn;
+          vc[prow + j] = vn;
+        }
+      }
+    }
+    __syncthreads();
+    float acc = 0.f;
+    if (mine && t == pos) {
+      for (int j = 0; j < D; ++j) acc += qs[j] * knew[j];
+    } else {
+#pragma unroll
+      for (int j = 0; j < D / 8; ++j)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc += qs[8 * j + e] * (float)kv[j][e];
+    }
+    const float sc = t < n ? acc * scale : -INFINITY;
+    const float m = wave_max(sc);
+    const float p = t < n ? expf(sc - m) : 0.f;
+    const float l = wave_sum(p);
+    if (mine && t == pos) {
+      for (int j = 0; j < D; ++j) pv[lane * (D + 1) + j] = p * vnew[j];
+    } else {
+#pragma unroll
+      for (int j = 0; j < D / 8; ++j)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) pv[lane * (D + 1) + 8 * j + e] = p * (float)vv[j][e];
+    }
+    __syncthreads();
+    for (int col = lane; col < D; col += 64) {
+      float o = 0.f;
+#pragma unroll 16
+      for (int u = 0; u < kSplit; ++u) o += pv[u * (D + 1) + col];
+      put(rec + 2 + col, o);
+    }
+    if (lane == 0) { put(rec, m); put(rec + 1, l); }
+  }
+  // every record store has completed before the arrival is counted
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  if (lane == 0) s_arrived = __hip_atomic_fetch_add(cnt + h, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  __syncthreads();
+  if (s_arrived != (unsigned)(nsplit - 1)) return;
+  // the last workgroup of head h: combine the splits in split order
+  auto get = [&](const float* a) { return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM); };
+  const float* base = ws + (int64_t)h * nsplit * (D + 2);
+  const float mc = lane < nsplit ? get(base + lane * (D + 2)) : -INFINITY;
+  const float lc = lane < nsplit ? get(base + lane * (D + 2) + 1) : 0.f;
+  const float mm = wave_max(mc);
+  const float wc = mc != -INFINITY ? expf(mc - mm) : 0.f;
+  wgt[lane] = wc;   // l and o are summed in split order
+  __syncthreads();
+  float ll = 0.f;
+  for (int cc = 0; cc < nsplit; ++cc) ll += __shfl(lc, cc) * wgt[cc];
+  constexpr int CPL = D / 64;
+  float o[CPL] = {};
+  for (int c0 = 0; c0 < nsplit; c0 += 8) {   // eight splits' loads in flight at a time
+    float v[8][CPL];
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+#pragma unroll
+      for (int e = 0; e < CPL; ++e)
+        v[k][e] = c0 + k < nsplit ? get(base + (c0 + k) * (D + 2) + 2 + CPL * lane + e) : 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      if (c0 + k < nsplit)
+#pragma unroll
+        for (int e = 0; e < CPL; ++e) o[e] += v[k][e] * wgt[c0 + k];
+  }
+#pragma unroll
+  for (int e = 0; e < CPL; ++e) out[h * D + CPL * lane + e] = (_Float16)(o[e] / ll);
+  if (lane == 0) __hip_atomic_store(cnt + h, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 }  // namespace
 
 hipError_t add_rmsnorm_launch(void* x, const void* delta, const void* w, void* out, int rows, int n, float eps,
                               hipStream_t s) {
+  if (n <= 8 * 1024 && n % 8 == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)w & 15) == 0 &&
+      ((uintptr_t)out & 15) == 0 && ((uintptr_t)delta & 15) == 0) {
+    const int nt = std::min(1024, (n / 8 + 63) / 64 * 64);
+    hipLaunchKernelGGL(add_rmsnorm_reg_kernel, dim3(rows), dim3(nt), 0, s, (_Float16*)x, (const _Float16*)delta,
+                       (const _Float16*)w, (_Float16*)out, n, eps);
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(rows), dim3(1024), 0, s, (_Float16*)x, (const _Float16*)delta,
                      (const _Float16*)w, (_Float16*)out, n, eps);
   return hipGetLastError();
@@ -182,11 +433,47 @@ size_t attn_decode_workspace(int H, int D, int64_t L) {
 hipError_t attn_decode_launch(const void* q, const void* kc, const void* vc, const int64_t* pos, void* out, int H,
                               int KVH, int D, int64_t L, float scale, void* ws, hipStream_t s) {
   const int nsplit = (int)((L + kSplit - 1) / kSplit);
-  hipLaunchKernelGGL(attn_partial_kernel, dim3(nsplit, H), dim3(64), 0, s, (const _Float16*)q, (const _Float16*)kc,
-                     (const _Float16*)vc, pos, (float*)ws, H, KVH, D, L, scale);
+  if (D == 128)
+    hipLaunchKernelGGL(attn_partial_d_kernel<128>, dim3(nsplit, H), dim3(64), 0, s, (const _Float16*)q,
+                       (const _Float16*)kc, (const _Float16*)vc, pos, (float*)ws, H, KVH, L, scale);
+  else if (D == 64)
+    hipLaunchKernelGGL(attn_partial_d_kernel<64>, dim3(nsplit, H), dim3(64), 0, s, (const _Float16*)q,
+                       (const _Float16*)kc, (const _Float16*)vc, pos, (float*)ws, H, KVH, L, scale);
+  else
+    hipLaunchKernelGGL(attn_partial_kernel, dim3(nsplit, H), dim3(64), 0, s, (const _Float16*)q, (const _Float16*)kc,
+                       (const _Float16*)vc, pos, (float*)ws, H, KVH, D, L, scale);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(attn_combine_kernel, dim3(H), dim3(128), 0, s, (const float*)ws, (_Float16*)out, nsplit, D);
+  if (nsplit <= 64)
+    hipLaunchKernelGGL(attn_combine_wave_kernel, dim3(H), dim3(64), 0, s, (const float*)ws, (_Float16*)out, nsplit, D);
+  else
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(H), dim3(128), 0, s, (const float*)ws, (_Float16*)out, nsplit, D);
+  return hipGetLastError();
+}
+
+size_t attn_fused_workspace(int H, int D, int64_t L) {
+  // per-head counters first (256-byte aligned), then the split records
+  return 256 * (((size_t)H * 4 + 255) / 256) + attn_decode_workspace(H, D, L);
+}
+
+bool attn_fused_supported(int H, int D, int64_t L) {
+  return H >= 1 && (D == 64 || D == 128) && (L + kSplit - 1) / kSplit <= 64;
+}
+
+hipError_t attn_fused_launch(const void* qkv, const float* cos_t, const float* sin_t, const int64_t* pos, void* kc,
+                             void* vc, void* out, int H, int KVH, int D, int64_t L, float scale, void* ws,
+                             hipStream_t s) {
+  const int nsplit = (int)((L + kSplit - 1) / kSplit);
+  unsigned int* cnt = (unsigned int*)ws;
+  float* rec = (float*)((unsigned char*)ws + 256 * (((size_t)H * 4 + 255) / 256));
+  if (D == 128)
+    hipLaunchKernelGGL(attn_fused_d_kernel<128>, dim3(nsplit, H), dim3(64), 0, s, (const _Float16*)qkv, cos_t, sin_t,
+                       pos, (_Float16*)kc, (_Float16*)vc, (_Float16*)out, rec, cnt, H, KVH, L, scale);
+  else if (D == 64)
+    hipLaunchKernelGGL(attn_fused_d_kernel<64>, dim3(nsplit, H), dim3(64), 0, s, (const _Float16*)qkv, cos_t, sin_t,
+                       pos, (_Float16*)kc, (_Float16*)vc, (_Float16*)out, rec, cnt, H, KVH, L, scale);
+  else
+    return hipErrorInvalidValue;
   return hipGetLastError();
 }
 

@@ -49,6 +49,10 @@ SIGNATURES = {
     "mq_rope_kv_f16": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                               _i32, _i32, _i32, _i64, _c_void_p]),
     "mq_attention_decode_workspace_size": (_i64, [_i32, _i32, _i64]),
+    "mq_attention_decode_rope_workspace_size": (_i64, [_i32, _i32, _i64]),
+    "mq_attention_decode_rope_f16": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                            _c_void_p, _i32, _i32, _i32, _i64, ctypes.c_float, _c_void_p, _i64,
+                                            _c_void_p]),
     "mq_attention_decode_f16": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i32, _i32, _i32,
                                        _i64, ctypes.c_float, _c_void_p, _i64, _c_void_p]),
     "mq_set_option": (_i32, [ctypes.c_char_p, _i64]),

@@ -131,11 +131,14 @@ class SyntheticDecoder:
                                                         device=self.device, generator=gen)).half()
         self.prefilled = prefilled
         self.positions = torch.arange(cfg.max_len, device=self.device)
+        # fused rotary + attention workspace (per-head counters start at zero)
+        self.attn_ws = ops.attention_decode_rope_workspace(cfg.heads, cfg.head_dim, cfg.max_len, self.device)
 
     # one decode step: token [1] int64, pos [1] int64 (device tensors) -> next token [1]
     def step(self, token: torch.Tensor, pos: torch.Tensor, return_logits: bool = False):
-        """Eight launches per layer: add+RMSNorm, QKV (+bias), RoPE + cache
-        write, attention, o_proj, add+RMSNorm, gate/up (+SwiGLU), down."""
+        """Six launches per layer: add+RMSNorm, QKV (+bias), RoPE + cache
+        write + attention (one kernel), o_proj, add+RMSNorm, gate/up
+        (+SwiGLU), down."""
         cfg = self.cfg
         H, KVH, Dh = cfg.heads, cfg.kv_heads, cfg.head_dim
         scale = 1.0 / math.sqrt(Dh)
@@ -144,8 +147,8 @@ class SyntheticDecoder:
         for li, L in enumerate(self.layers):
             h = ops.add_rmsnorm(x, delta, L["ln1"], cfg.eps)        # x += delta; h = norm(x)
             qkv = L["qkv"](h)
-            q = ops.rope_kv(qkv, self.cos, self.sin, pos, self.kv[li, 0], self.kv[li, 1], H, KVH, Dh)
-            a = ops.attention_decode(q, self.kv[li, 0], self.kv[li, 1], pos, scale)
+            a = ops.attention_decode_rope(qkv, self.cos, self.sin, pos, self.kv[li, 0], self.kv[li, 1], H, KVH, Dh,
+                                          scale, self.attn_ws)
             h = ops.add_rmsnorm(x, L["o"](a), L["ln2"], cfg.eps)
             delta = L["down"](L["gate_up"](h, epilogue="swiglu"))
         logits = self.lm_head(ops.add_rmsnorm(x, delta, self.norm, cfg.eps))   # [1, vocab]

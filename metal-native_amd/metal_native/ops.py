@@ -406,6 +406,31 @@ def attention_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
     return out
 
 
+def attention_decode_rope_workspace(heads: int, head_dim: int, max_len: int, device) -> torch.Tensor | None:
+    """Zeroed workspace for ``attention_decode_rope`` (None when the fused
+    kernel does not take the shape); keep one per stream."""
+    nb = _L.mq_attention_decode_rope_workspace_size(heads, head_dim, max_len)
+    if nb < 0:
+        return None
+    return torch.zeros(nb, dtype=torch.uint8, device=device)
+
+
+def attention_decode_rope(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, pos: torch.Tensor,
+                          k_cache: torch.Tensor, v_cache: torch.Tensor, heads: int, kv_heads: int, head_dim: int,
+                          scale: float, workspace: torch.Tensor | None) -> torch.Tensor:
+    """``rope_kv`` followed by ``attention_decode``: one launch with a
+    workspace from ``attention_decode_rope_workspace``, else (None) the two
+    separate kernels."""
+    if workspace is None:
+        q = rope_kv(qkv, cos, sin, pos, k_cache, v_cache, heads, kv_heads, head_dim)
+        return attention_decode(q, k_cache, v_cache, pos, scale)
+    out = torch.empty((1, heads * head_dim), dtype=torch.float16, device=qkv.device)
+    _check(_L.mq_attention_decode_rope_f16(_ptr(qkv), _ptr(cos), _ptr(sin), _ptr(pos), _ptr(k_cache), _ptr(v_cache),
+                                           _ptr(out), heads, kv_heads, head_dim, k_cache.shape[1], float(scale),
+                                           _ptr(workspace), workspace.numel(), _stream_handle(qkv.device)))
+    return out
+
+
 def synchronize() -> None:
     """``_C.synchronize``: wait for all queued GPU work."""
     torch.cuda.synchronize()

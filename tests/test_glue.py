@@ -1,0 +1,119 @@
+"""Decoder glue kernels against fp32 torch restatements, at the config-5
+shapes (d = 3584, 28 query / 4 KV heads of 128, 576-position cache) and a
+small one (head_dim 64), including a position at the end of the cache."""
+
+import math
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return torch.device("cuda:0")
+
+
+@pytest.mark.parametrize("rows,n", [(1, 3584), (3, 256), (2, 9000)])
+@pytest.mark.parametrize("with_delta", [True, False])
+def test_add_rmsnorm(gpu, rows, n, with_delta):
+    from metal_native import ops
+
+    g = torch.Generator(device=gpu)
+    g.manual_seed(n + rows)
+    x = torch.randn((rows, n), device=gpu, generator=g).half()
+    d = torch.randn((rows, n), device=gpu, generator=g).half() if with_delta else None
+    w = (torch.randn(n, device=gpu, generator=g) * 0.1).half()
+    x0 = x.clone()
+    out = ops.add_rmsnorm(x, d, w, 1e-6)
+    xs = (x0.float() + d.float()).half() if with_delta else x0
+    assert torch.equal(x, xs)                                       # residual written back (fp16 add)
+    xf = xs.float()
+    ref = (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-6) * w.float()).half()
+    err = (out.float() - ref.float()).abs()
+    assert float(err.max()) <= 2e-3 + 2e-3 * float(ref.float().abs().max())
+
+
+def attention_ref(q, kc, vc, pos, scale):
+    H, D = q.shape
+    KVH = kc.shape[0]
+    grp = H // KVH
+    k = kc[:, : pos + 1].float()
+    v = vc[:, : pos + 1].float()
+    s = torch.matmul(q.view(KVH, grp, D).float(), k.transpose(1, 2)) * scale
+    return torch.matmul(torch.softmax(s, dim=-1), v).reshape(1, H * D)
+
+
+@pytest.mark.parametrize("H,KVH,D,L,pos", [(28, 4, 128, 576, 512), (28, 4, 128, 576, 575), (28, 4, 128, 576, 0),
+                                           (4, 2, 64, 32, 17), (8, 8, 64, 200, 130), (6, 2, 96, 80, 70)])
+def test_attention_decode(gpu, H, KVH, D, L, pos):
+    from metal_native import ops
+
+    g = torch.Generator(device=gpu)
+    g.manual_seed(H * D + pos)
+    q = torch.randn((H, D), device=gpu, generator=g).half()
+    kc = torch.randn((KVH, L, D), device=gpu, generator=g).half()
+    vc = torch.randn((KVH, L, D), device=gpu, generator=g).half()
+    p = torch.tensor([pos], device=gpu)
+    scale = 1.0 / math.sqrt(D)
+    out = ops.attention_decode(q, kc, vc, p, scale)
+    ref = attention_ref(q, kc, vc, pos, scale)
+    err = (out.float() - ref).abs()
+    assert float(err.max()) <= 3e-3 + 3e-3 * float(ref.abs().max()), float(err.max())
+
+
+@pytest.mark.parametrize("H,KVH,D,L,pos", [(28, 4, 128, 576, 512), (4, 2, 64, 32, 31)])
+def test_rope_kv(gpu, H, KVH, D, L, pos):
+    from metal_native import ops
+    from metal_native.decoder import DecoderConfig, apply_rope, rope_tables
+
+    cfg = DecoderConfig(heads=H, kv_heads=KVH, head_dim=D, max_len=L)
+    cos, sin = rope_tables(cfg, gpu)
+    g = torch.Generator(device=gpu)
+    g.manual_seed(pos)
+    qkv = torch.randn((1, (H + 2 * KVH) * D), device=gpu, generator=g).half()
+    kc = torch.zeros((KVH, L, D), device=gpu, dtype=torch.float16)
+    vc = torch.zeros_like(kc)
+    q = ops.rope_kv(qkv, cos, sin, torch.tensor([pos], device=gpu), kc, vc, H, KVH, D)
+    flat = qkv[0]
+    rq = apply_rope(flat[: H * D].view(H, D), cos[pos], sin[pos])
+    rk = apply_rope(flat[H * D:(H + KVH) * D].view(KVH, D), cos[pos], sin[pos])
+    assert (q.float() - rq.float()).abs().max() <= 2e-3
+    assert (kc[:, pos].float() - rk.float()).abs().max() <= 2e-3
+    assert torch.equal(vc[:, pos], flat[(H + KVH) * D:].view(KVH, D))
+    assert float(kc[:, :pos].abs().sum()) == 0 and float(vc[:, pos + 1:].abs().sum()) == 0
+
+
+@pytest.mark.parametrize("H,KVH,D,L,pos", [(28, 4, 128, 576, 512), (28, 4, 128, 576, 575), (28, 4, 128, 576, 63),
+                                           (4, 2, 64, 32, 17), (8, 8, 64, 200, 0)])
+def test_fused_rope_attention_matches_separate_kernels(gpu, H, KVH, D, L, pos):
+    """One launch (rotary + cache write + attention + combine) against the
+    separate rope_kv and attention_decode kernels: same output up to the
+    split-combine order, same cache contents, on three successive calls on
+    one workspace (the per-head counters must be left at zero)."""
+    from metal_native import ops
+    from metal_native.decoder import DecoderConfig, rope_tables
+
+    cfg = DecoderConfig(heads=H, kv_heads=KVH, head_dim=D, max_len=L)
+    cos, sin = rope_tables(cfg, gpu)
+    g = torch.Generator(device=gpu)
+    g.manual_seed(pos + D)
+    kc0 = torch.randn((KVH, L, D), device=gpu, generator=g).half()
+    vc0 = torch.randn((KVH, L, D), device=gpu, generator=g).half()
+    ws = ops.attention_decode_rope_workspace(H, D, L, gpu)
+    assert ws is not None
+    scale = 1.0 / math.sqrt(D)
+    for rep in range(3):
+        qkv = torch.randn((1, (H + 2 * KVH) * D), device=gpu, generator=g).half()
+        p = torch.tensor([pos], device=gpu)
+        k1, v1 = kc0.clone(), vc0.clone()
+        q = ops.rope_kv(qkv, cos, sin, p, k1, v1, H, KVH, D)
+        want = ops.attention_decode(q, k1, v1, p, scale)
+        k2, v2 = kc0.clone(), vc0.clone()
+        got = ops.attention_decode_rope(qkv, cos, sin, p, k2, v2, H, KVH, D, scale, ws)
+        assert torch.equal(k1, k2) and torch.equal(v1, v2)
+        err = (got.float() - want.float()).abs()
+        assert float(err.max()) <= 1e-3 * (1 + float(want.float().abs().max())), (rep, float(err.max()))
