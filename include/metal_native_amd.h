@@ -80,6 +80,22 @@ MQ_API int mq_dequantize(const void* weights_packed, int64_t ldw_bytes, const vo
                          const void* zeros, void* out, int64_t ldo, int64_t N, int64_t K,
                          int32_t group_size, int32_t quant_type, int32_t flat_groups, void* stream);
 
+/* Residual add + RMSNorm fused into the decode GEMV (M = 1; no reference
+ * counterpart: the decode step's glue).  x, delta (may be NULL), norm_weight,
+ * resid_out fp16 [K] (16-byte aligned; resid_out must not alias x or delta):
+ *   resid_out = half(x + delta);  h = half(resid_out * rsqrt(mean(resid_out^2)
+ *   + eps) * norm_weight);  C = epilogue(h . deq(W)^T)  as mq_dequant_matmul.
+ * Runs only where the row-block kernel takes the shape
+ * (mq_rmsnorm_dequant_matmul_supported); otherwise returns 4 and the caller
+ * runs mq_add_rmsnorm_f16 and mq_dequant_matmul. */
+MQ_API int mq_rmsnorm_dequant_matmul(const void* x, const void* delta, const void* norm_weight, float eps,
+                                     void* resid_out, const void* weights_packed, int64_t ldw_bytes,
+                                     const void* scales, const void* zeros, void* C, int64_t N, int64_t K,
+                                     int32_t group_size, int32_t quant_type, int32_t epilogue, const void* bias,
+                                     void* stream);
+MQ_API int mq_rmsnorm_dequant_matmul_supported(int64_t N, int64_t K, int32_t group_size, int32_t quant_type,
+                                               int32_t epilogue);
+
 /* Group quantizer, the inverse of the dequant formula (no reference
  * counterpart: the reference has no quantizer and its tests pack weights by
  * hand, tests/cpp/test_dequant_matmul.mm:104-116).  w fp16 [N, K] (row stride

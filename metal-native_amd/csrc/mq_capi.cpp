@@ -199,6 +199,48 @@ MQ_API int mq_dequant_matmul(const void* activations, int64_t lda, const void* w
   return run_linear(a, (hipStream_t)stream);
 }
 
+MQ_API int mq_rmsnorm_dequant_matmul(const void* x, const void* delta, const void* norm_weight, float eps,
+                                     void* resid_out, const void* weights_packed, int64_t ldw_bytes,
+                                     const void* scales, const void* zeros, void* C, int64_t N, int64_t K,
+                                     int32_t group_size, int32_t quant_type, int32_t epilogue, const void* bias,
+                                     void* stream) {
+  if (!x || !norm_weight || !resid_out)
+    return fail(MQ_INVALID_ARGUMENT, "rmsnorm_dequant_matmul: null pointer argument");
+  if (resid_out == x || (delta && resid_out == delta))
+    return fail(MQ_INVALID_ARGUMENT, "rmsnorm_dequant_matmul: resid_out must not alias x or delta");
+  mq::LinearArgs a{};
+  int rc = build_args(a, 1, N, K, group_size, quant_type, epilogue);
+  if (rc != MQ_SUCCESS) return rc;
+  a.A = x; a.lda = K;
+  a.W = weights_packed; a.ldw = ldw_bytes;
+  a.scales = scales; a.zeros = zeros; a.bias = bias;
+  a.C = C; a.ldc = a.epi == mq::EPI_SWIGLU ? a.F : N;
+  a.prenorm = 1; a.pre_delta = delta; a.pre_weight = norm_weight; a.pre_resid = resid_out; a.pre_eps = eps;
+  if (!weights_packed || !scales || !C) return fail(MQ_INVALID_ARGUMENT, "rmsnorm_dequant_matmul: null pointer argument");
+  if (epilogue == MQ_EPILOGUE_BIAS && !bias)
+    return fail(MQ_INVALID_ARGUMENT, "rmsnorm_dequant_matmul: bias epilogue needs a bias pointer");
+  if (ldw_bytes < (quant_type == MQ_QUANT_INT4 ? K / 2 : K))
+    return fail(MQ_INVALID_ARGUMENT, "rmsnorm_dequant_matmul: weight rows too short");
+  const mq::RowsPlan pl = mq::rows_plan(a, num_cus_current());
+  if (!pl.ok) return fail(MQ_INVALID_ARGUMENT, "rmsnorm_dequant_matmul: shape not supported by the fused kernel");
+  hipError_t e = mq::rows_launch(a, pl, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "rmsnorm_dequant_matmul: kernel launch failed");
+  g_last_path = PATH_ROWS;
+  return MQ_SUCCESS;
+}
+
+MQ_API int mq_rmsnorm_dequant_matmul_supported(int64_t N, int64_t K, int32_t group_size, int32_t quant_type,
+                                               int32_t epilogue) {
+  mq::LinearArgs a{};
+  if (build_args(a, 1, N, K, group_size, quant_type, epilogue) != MQ_SUCCESS) return 0;
+  static const uint64_t kAligned[2] = {0, 0};  // stand-in pointers: only the shape is asked about
+  a.A = a.W = a.scales = kAligned;
+  a.lda = K;
+  a.ldw = quant_type == MQ_QUANT_INT4 ? K / 2 : K;
+  a.prenorm = 1; a.pre_weight = a.pre_resid = (void*)kAligned;
+  return mq::rows_plan(a, num_cus_current()).ok ? 1 : 0;
+}
+
 MQ_API int mq_dequantize(const void* weights_packed, int64_t ldw_bytes, const void* scales,
                          const void* zeros, void* out, int64_t ldo, int64_t N, int64_t K,
                          int32_t group_size, int32_t quant_type, int32_t flat_groups, void* stream) {

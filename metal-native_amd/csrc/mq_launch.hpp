@@ -26,6 +26,14 @@ struct LinearArgs {
   int fmt;              // Fmt
   int epi;              // Epi
   int F;                // SwiGLU half width (N = 2F), 0 otherwise
+  // Optional fused pre-norm (row-block GEMV, M = 1): the activations are
+  // A' = half(A + pre_delta) (pre_delta may be null), written to pre_resid by
+  // one workgroup, then RMS-normalised: half(A' * rsqrt(mean(A'^2) + eps) * w).
+  int prenorm = 0;
+  const void* pre_delta = nullptr;
+  const void* pre_weight = nullptr;
+  void* pre_resid = nullptr;
+  float pre_eps = 0.f;
 };
 
 // Split-K MFMA GEMV (decode, M <= 16).

@@ -77,9 +77,11 @@ struct RowsKArgs {
   uint32_t off_sz, off_scr, off_slot;  // LDS byte offsets
   uint32_t a_bytes, sz_bytes, z_bytes;
   uint64_t ppr_magic;  // ceil(2^32 / ppr): idx / ppr = (idx * magic) >> 32 for the staged index range
+  const _Float16* pre_delta; const _Float16* pre_weight; _Float16* pre_resid;  // fused pre-norm (PRE)
+  float pre_eps;
 };
 
-template <int FMT, int EPI, int RPW>
+template <int FMT, int EPI, int RPW, bool PRE>
 __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
   constexpr int S = 16 / RPW;
   constexpr int KPL = FmtTraits<FMT>::KPL;       // k per 16-byte piece
@@ -275,7 +277,21 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
   {
     u4 xv[kXB];
     u4 sv[kSB], zv[kSB];
+    u4 dv[PRE ? kXB : 1], wv[PRE ? kXB : 1];
     x_fetch(0, xv, nxb);
+    if (PRE) {  // residual delta and norm weight pieces, same indices (M = 1: piece c at 16c bytes)
+      const rsrc_t dr = make_rsrc(p.pre_delta, p.pre_delta ? (uint32_t)(p.K * 2) : 0u);
+      const rsrc_t nr = make_rsrc(p.pre_weight, (uint32_t)(p.K * 2));
+#pragma unroll
+      for (int e = 0; e < kXB; ++e) {
+        if (e < nxb) {
+          const int idx = tid + e * NT;
+          const uint32_t off = (idx < npieces && 8 * idx < p.K) ? (uint32_t)(idx * 16) : kOob;
+          dv[e] = bload16(dr, off);
+          wv[e] = bload16(nr, off);
+        }
+      }
+    }
     if (FMT != FMT_F16) s_fetch(0, sv, zv, nsb);
     // every wave's staging loads reach the texture unit first (a plain
     // barrier: it does not wait for the loads) ...
@@ -291,6 +307,48 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
 #pragma unroll
     for (int e = 0; e < kSB; ++e) asm volatile("" : "+v"(sv[e]), "+v"(zv[e]));
     MQ_TRACE(6);
+    if (PRE) {
+      // A' = half(A + delta) (the residual, stored by workgroup 0), then the
+      // row's sum of squares across the workgroup, then the normalised pieces
+      float ss = 0.f;
+#pragma unroll
+      for (int e = 0; e < kXB; ++e) {
+        if (e < nxb) {
+          asm volatile("" : "+v"(dv[e]), "+v"(wv[e]));
+          h8 v = __builtin_bit_cast(h8, xv[e]);
+          if (p.pre_delta) {
+            const h8 d = __builtin_bit_cast(h8, dv[e]);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) v[k] = (_Float16)((float)v[k] + (float)d[k]);
+          }
+#pragma unroll
+          for (int k = 0; k < 8; ++k) ss += (float)v[k] * (float)v[k];
+          xv[e] = __builtin_bit_cast(u4, v);
+          const int idx = tid + e * NT;
+          if (b == 0 && idx < npieces && 8 * idx < p.K) *(h8*)(p.pre_resid + 8 * idx) = v;
+        }
+      }
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+      float* red = (float*)(smem + p.off_scr);   // per-wave scratch, free until the first tile fold
+      if (lane == 0) red[w * 256] = ss;
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      float tot = 0.f;
+#pragma unroll
+      for (int ww = 0; ww < NW; ++ww) tot += red[ww * 256];
+      const float rn = rsqrtf(tot / (float)p.K + p.pre_eps);
+#pragma unroll
+      for (int e = 0; e < kXB; ++e) {
+        if (e < nxb) {
+          const h8 v = __builtin_bit_cast(h8, xv[e]);
+          const h8 wn = __builtin_bit_cast(h8, wv[e]);
+          h8 o8;
+#pragma unroll
+          for (int k = 0; k < 8; ++k) o8[k] = (_Float16)((float)v[k] * rn * (float)wn[k]);
+          xv[e] = __builtin_bit_cast(u4, o8);
+        }
+      }
+    }
     x_put(0, xv, nxb);
     if (FMT != FMT_F16) s_put(0, sv, zv, nsb);
 #pragma unroll
@@ -431,10 +489,10 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
   MQ_TRACE(4);
 }
 
-template <int FMT, int EPI, int RPW>
-hipError_t launch3(const RowsKArgs& k, const RowsPlan& pl, hipStream_t s) {
+template <int FMT, int EPI, int RPW, bool PRE>
+hipError_t launch4(const RowsKArgs& k, const RowsPlan& pl, hipStream_t s) {
   static bool attr = false;
-  auto fn = rows_kernel<FMT, EPI, RPW>;
+  auto fn = rows_kernel<FMT, EPI, RPW, PRE>;
   if (!attr) {
     hipError_t e = hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLds);
     if (e != hipSuccess) return e;
@@ -442,6 +500,14 @@ hipError_t launch3(const RowsKArgs& k, const RowsPlan& pl, hipStream_t s) {
   }
   hipLaunchKernelGGL(fn, dim3(pl.nwg), dim3(64 * kNW), pl.lds_bytes, s, k);
   return hipGetLastError();
+}
+
+template <int FMT, int EPI, int RPW>
+hipError_t launch3(const RowsKArgs& k, const RowsPlan& pl, hipStream_t s) {
+  if constexpr (FMT != FMT_F16) {
+    if (k.pre_weight) return launch4<FMT, EPI, RPW, true>(k, pl, s);
+  }
+  return launch4<FMT, EPI, RPW, false>(k, pl, s);
 }
 
 template <int FMT, int EPI>
@@ -530,6 +596,11 @@ RowsPlan rows_plan(const LinearArgs& a, int num_cus) {
   off += al16((size_t)nw * maxT * a.M * rpw * 4);
   if (off > kLds) return p;
   if ((int64_t)U * nw >= ((int64_t)1 << 31)) return p;  // unit ranges in 32-bit arithmetic
+  if (a.prenorm) {  // one staging batch, whole 16-byte pieces, M = 1
+    const int64_t pieces = (int64_t)KS * kstep / 8;
+    if (a.M != 1 || !quant || a.K % 8 || pieces > (int64_t)kXB * 64 * nw || !a.pre_weight || !a.pre_resid) return p;
+    if (((uintptr_t)a.pre_weight | (uintptr_t)a.pre_resid | (uintptr_t)a.pre_delta) & 15) return p;
+  }
   {
     // idx / d = (idx * ceil(2^32/d)) >> 32 is exact while idx * e < 2^32,
     // e = ceil(2^32/d)*d - 2^32 < d; the staged index ranges are far below
@@ -557,6 +628,12 @@ hipError_t rows_launch(const LinearArgs& a, const RowsPlan& pl, hipStream_t s) {
   k.gshift = gshift_of(a);
   k.R = pl.R; k.TW = pl.TW; k.KS = pl.KS; k.XS = pl.XS; k.maxT = pl.maxT; k.szrows = pl.szrows; k.szpad = pl.szpad;
   k.off_sz = pl.off_sz; k.off_scr = pl.off_scr; k.off_slot = pl.off_slot;
+  if (a.prenorm) {
+    k.pre_delta = (const _Float16*)a.pre_delta;
+    k.pre_weight = (const _Float16*)a.pre_weight;
+    k.pre_resid = (_Float16*)a.pre_resid;
+    k.pre_eps = a.pre_eps;
+  }
   k.a_bytes = (uint32_t)(((int64_t)(a.M - 1) * a.lda + a.K) * 2);
   k.sz_bytes = a.fmt == FMT_F16 ? 0u : (uint32_t)(((int64_t)a.N * a.G * 2 + 3) & ~(int64_t)3);
   k.z_bytes = a.zeros ? k.sz_bytes : 0u;

@@ -12,8 +12,9 @@ projection is an int4 g128 ``dequant_matmul``:
 * gate/up: one fused call with the SwiGLU epilogue (gate rows, then up rows);
 * down_proj and the lm_head.
 
-Residual add + RMSNorm, rotary embedding + KV-cache write and single-token
-grouped-query attention are the library's glue kernels (mq_glue.hip); the
+Residual add + RMSNorm runs inside the following GEMV (the row-block
+kernel's staging), rotary embedding + KV-cache write + single-token
+grouped-query attention is one glue kernel (mq_glue.hip); the
 embedding lookup and the greedy argmax are PyTorch ops on the same stream.
 The decode step has static shapes (the position is a device tensor), so a
 whole step is captured in a HIP graph and replayed token after token.
@@ -70,6 +71,10 @@ class QLinear:
         z = ((zp - 8.0) * s.float()).half()
         b = (torch.randn(n, device=device, generator=gen) * 0.02).half() if bias else None
         return QLinear(wp, s, z, g, b)
+
+    def operands(self):
+        """(weights_packed, scales, zeros, group_size, quant_type) for the ops."""
+        return self.wp, self.scales, self.zeros, self.g, "int4"
 
     def __call__(self, x: torch.Tensor, epilogue: str | None = None) -> torch.Tensor:
         if self.bias is not None and epilogue is None:
@@ -131,27 +136,38 @@ class SyntheticDecoder:
                                                         device=self.device, generator=gen)).half()
         self.prefilled = prefilled
         self.positions = torch.arange(cfg.max_len, device=self.device)
+        # two residual-stream buffers (the fused norm + GEMV writes out of place)
+        self.resid = torch.zeros((2, 1, d), dtype=torch.float16, device=self.device)
         # fused rotary + attention workspace (per-head counters start at zero)
         self.attn_ws = ops.attention_decode_rope_workspace(cfg.heads, cfg.head_dim, cfg.max_len, self.device)
 
     # one decode step: token [1] int64, pos [1] int64 (device tensors) -> next token [1]
     def step(self, token: torch.Tensor, pos: torch.Tensor, return_logits: bool = False):
-        """Six launches per layer: add+RMSNorm, QKV (+bias), RoPE + cache
-        write + attention (one kernel), o_proj, add+RMSNorm, gate/up
-        (+SwiGLU), down."""
+        """Five launches per layer: QKV with the residual add + RMSNorm fused
+        into it (+bias), RoPE + cache write + attention (one kernel), o_proj,
+        gate/up with the residual add + RMSNorm fused (+SwiGLU), down.  The
+        residual stream alternates between two buffers (the fused kernel
+        reads x and writes the new residual elsewhere)."""
         cfg = self.cfg
         H, KVH, Dh = cfg.heads, cfg.kv_heads, cfg.head_dim
         scale = 1.0 / math.sqrt(Dh)
         x = self.embed.index_select(0, token)                      # [1, d] residual stream
+        bufs = (self.resid[0], self.resid[1])
+        cur = 0
         delta = None
         for li, L in enumerate(self.layers):
-            h = ops.add_rmsnorm(x, delta, L["ln1"], cfg.eps)        # x += delta; h = norm(x)
-            qkv = L["qkv"](h)
+            qkv = ops.rmsnorm_dequant_matmul(x, delta, L["ln1"], cfg.eps, bufs[cur], *L["qkv"].operands(),
+                                             epilogue="bias", bias=L["qkv"].bias)
+            x = bufs[cur]
+            cur ^= 1
             a = ops.attention_decode_rope(qkv, self.cos, self.sin, pos, self.kv[li, 0], self.kv[li, 1], H, KVH, Dh,
                                           scale, self.attn_ws)
-            h = ops.add_rmsnorm(x, L["o"](a), L["ln2"], cfg.eps)
-            delta = L["down"](L["gate_up"](h, epilogue="swiglu"))
-        logits = self.lm_head(ops.add_rmsnorm(x, delta, self.norm, cfg.eps))   # [1, vocab]
+            act = ops.rmsnorm_dequant_matmul(x, L["o"](a), L["ln2"], cfg.eps, bufs[cur], *L["gate_up"].operands(),
+                                             epilogue="swiglu")
+            x = bufs[cur]
+            cur ^= 1
+            delta = L["down"](act)
+        logits = ops.rmsnorm_dequant_matmul(x, delta, self.norm, cfg.eps, bufs[cur], *self.lm_head.operands())
         nxt = torch.argmax(logits.float(), dim=-1)
         return (nxt, logits) if return_logits else nxt
 

@@ -406,6 +406,36 @@ def attention_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
     return out
 
 
+def rmsnorm_dequant_matmul(x: torch.Tensor, delta: torch.Tensor | None, norm_weight: torch.Tensor, eps: float,
+                           resid_out: torch.Tensor, weights_packed: torch.Tensor, scales: torch.Tensor,
+                           zeros: torch.Tensor | None, group_size: int, quant_type: str, epilogue: str | None = None,
+                           bias: torch.Tensor | None = None) -> torch.Tensor:
+    """Decode step glue fused into the GEMV (one row): ``resid_out =
+    half(x + delta)``, ``h = half(resid_out * rsqrt(mean(resid_out^2) + eps) *
+    norm_weight)``, returns ``dequant_matmul(h, ...)``.  One launch where the
+    row-block kernel takes the shape, else ``add_rmsnorm`` + ``dequant_matmul``."""
+    qt = quant_type_code(quant_type)
+    epi = _EPILOGUES[epilogue]
+    N, cols = weights_packed.shape
+    K = x.shape[-1]
+    if (x.numel() == K and resid_out is not x and resid_out is not delta
+            and _L.mq_rmsnorm_dequant_matmul_supported(N, K, group_size, qt, epi)):
+        n_out = N // 2 if epi == _lib.EPILOGUE_SWIGLU else N
+        out = torch.empty((1, n_out), dtype=torch.float16, device=x.device)
+        rc = _L.mq_rmsnorm_dequant_matmul(_ptr(x), _ptr(delta), _ptr(norm_weight), float(eps), _ptr(resid_out),
+                                          _ptr(weights_packed), _rows(weights_packed, "weights_packed", "dequant_matmul"),
+                                          _ptr(scales), _ptr(zeros), _ptr(out), N, K, group_size, qt, epi, _ptr(bias),
+                                          _stream_handle(x.device))
+        if rc == 0:
+            return out
+        if rc != 4:
+            _check(rc)
+    resid_out.copy_(x)
+    h = add_rmsnorm(resid_out, delta, norm_weight, eps)
+    return dequant_matmul(h.reshape(-1, K), weights_packed, scales, zeros, group_size, quant_type, epilogue=epilogue,
+                          bias=bias)
+
+
 def attention_decode_rope_workspace(heads: int, head_dim: int, max_len: int, device) -> torch.Tensor | None:
     """Zeroed workspace for ``attention_decode_rope`` (None when the fused
     kernel does not take the shape); keep one per stream."""

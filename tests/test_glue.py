@@ -117,3 +117,35 @@ def test_fused_rope_attention_matches_separate_kernels(gpu, H, KVH, D, L, pos):
         assert torch.equal(k1, k2) and torch.equal(v1, v2)
         err = (got.float() - want.float()).abs()
         assert float(err.max()) <= 1e-3 * (1 + float(want.float().abs().max())), (rep, float(err.max()))
+
+
+@pytest.mark.parametrize("N,K,epi", [(4608, 3584, "bias"), (2 * 18944, 3584, "swiglu"), (3584, 18944, None),
+                                     (1000, 256, None), (640, 512, "swiglu")])
+@pytest.mark.parametrize("with_delta", [True, False])
+def test_rmsnorm_fused_into_gemv(gpu, N, K, epi, with_delta):
+    """One launch (residual add + RMSNorm in the GEMV's staging) against
+    add_rmsnorm followed by dequant_matmul: the residual bit for bit, the
+    product within the matmul tolerance."""
+    import numpy as np
+
+    import metal_native as mn
+    from metal_native import ops
+    from oracle import mq_oracle as O
+
+    rng = np.random.default_rng(N + K)
+    x = torch.from_numpy(rng.standard_normal((1, K)).astype(np.float16)).to(gpu)
+    d = torch.from_numpy(rng.standard_normal((1, K)).astype(np.float16)).to(gpu) if with_delta else None
+    w = torch.from_numpy((rng.standard_normal(K) * 0.1 + 1).astype(np.float16)).to(gpu)
+    _, wp, s, z = O.make_int4_problem(1, K, N, 128, seed=K)
+    wp, s, z = (torch.from_numpy(t).to(gpu) for t in (wp, s, z))
+    b = torch.from_numpy(rng.standard_normal(N).astype(np.float16)).to(gpu) if epi == "bias" else None
+    assert ops._L.mq_rmsnorm_dequant_matmul_supported(N, K, 128, 0, ops._EPILOGUES[epi]) == 1
+    r1 = torch.empty_like(x)
+    y1 = ops.rmsnorm_dequant_matmul(x, d, w, 1e-6, r1, wp, s, z, 128, "int4", epilogue=epi, bias=b)
+    assert mn.last_path() == "rows"
+    r2 = x.clone()
+    h = ops.add_rmsnorm(r2, d, w, 1e-6)
+    y2 = mn.dequant_matmul(h, wp, s, z, 128, "int4", epilogue=epi, bias=b)
+    assert torch.equal(r1, r2)
+    err = (y1.float() - y2.float()).abs()
+    assert float(err.max()) <= 2e-2 + 2e-3 * float(y2.float().abs().max()), float(err.max())
