@@ -339,6 +339,8 @@ def main():
     ap.add_argument("--cpu-reps", type=int, default=10)
     ap.add_argument("--only", default=None, help="comma-separated config names (headline always runs)")
     ap.add_argument("--only-headline", action="store_true", help="measure the headline config only")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="run only the config-5 decode step and print its JSON (for profiling)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy (rocprof counter calibration)")
     args = ap.parse_args()
@@ -358,6 +360,9 @@ def main():
     device = torch.device("cuda:0")
     if args.copy_calib:
         copy_calibration(device)
+        return
+    if args.decode_only:
+        print(json.dumps(decode_bench(device)))
         return
     names = list(CONFIGS)
     if args.only_headline:
