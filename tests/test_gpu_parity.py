@@ -523,3 +523,39 @@ def test_gptq_checkpoint_through_the_kernels(mn, gpu):
     x = rng.standard_normal((M, K)).astype(np.float16)
     y = host(mn.dequant_matmul(dev(x, gpu), cw.packed, cw.scales, cw.zeros, g, "int4"))
     check_close(y, O.matmul_f32acc(x, O.dequant_int4(bp, ss, zz, K, g)), "gptq checkpoint")
+
+
+@pytest.mark.parametrize("M,K,N,g,qt,epi", [
+    (1, 896, 4867, 64, "int4", None),        # scale array ends mid 16-byte piece; last workgroup partial
+    (2, 384, 1001, 128, "int4", "bias"),     # G = 3 (odd), runs not 16-byte aligned
+    (1, 1152, 2 * 777, 128, "int4", "swiglu"),
+    (4, 640, 515, 32, "int4", None),
+    (1, 896, 3003, 64, "int8", None),
+    (1, 3584, 2 * 1001, 3584, "int8", "swiglu"),
+])
+def test_rows_kernel_ragged_runs(mn, gpu, M, K, N, g, qt, epi):
+    """Row-block kernel at shapes whose per-workgroup scale/zero runs start and
+    end inside 16-byte pieces and whose last workgroup has fewer rows."""
+    say(f"rows ragged M={M} K={K} N={N} g={g} {qt} {epi}")
+    if qt == "int4":
+        x, wp, s, z = O.make_int4_problem(M, K, N, g, seed=N)
+        Wd = O.dequant_int4(wp, s, z, K, g)
+    else:
+        x, wp, s, z, g = O.make_int8_problem(M, K, N, seed=N, g=g)
+        z = (np.random.default_rng(2).uniform(-0.01, 0.01, s.shape)).astype(np.float16)
+        Wd = O.dequant_int8(wp, s, z, K, g)
+    acc = O.matmul_f32acc(x, Wd)
+    kw = {}
+    if epi == "bias":
+        b = np.random.default_rng(N).standard_normal(N).astype(np.float16)
+        kw = dict(epilogue="bias", bias=dev(b, gpu))
+    elif epi == "swiglu":
+        kw = dict(epilogue="swiglu")
+    y, taken = run_dm(mn, gpu, x, wp, s, z, g, qt, "rows", **kw)
+    assert taken == "rows"
+    if epi == "swiglu":
+        check_swiglu(y, acc, "rows ragged swiglu")
+    elif epi == "bias":
+        check_close(y, acc + b.astype(np.float32), "rows ragged bias")
+    else:
+        check_close(y, acc, "rows ragged")
