@@ -156,16 +156,24 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
     const uint32_t ro = row_off(t);
     return ro == kOob ? kOobPart : ro + (uint32_t)(klane * BPK2 / 2);
   };
-  uint32_t lvo = lane_off(lt);
+  // fp16 weights: the last step reads no bytes past K (raw fp16 there may
+  // hold any bits); its lane part is lvo_last.  Quantized bytes past K (the
+  // next row's, row padding, or zeros past the range) dequantize to finite
+  // values that meet zero activations, so those lanes load unmasked.
+  const bool kpast = FMT == FMT_F16 && (KS - 1) * KSTEP + klane >= p.K;
+  uint32_t lvo = lane_off(lt), lvo_last = kpast ? kOobPart : lvo;
   auto wload = [&]() -> u4 {
     uint32_t so = kOobPart, vo = lvo;
     if (left > 0) {
       so = (uint32_t)(lj * (KSTEP * BPK2 / 2));
-      // the last step: no bytes past K (raw fp16 there may hold any bits, and
-      // quantized bytes there are wasted traffic)
-      if (lj == KS - 1 && lj * KSTEP + klane >= p.K) vo = kOobPart;
+      if (FMT == FMT_F16 && lj == KS - 1) vo = lvo_last;
       --left;
-      if (++lj == KS) { lj = 0; ++lt; lvo = lane_off(lt); }
+      if (++lj == KS) {
+        lj = 0;
+        ++lt;
+        lvo = lane_off(lt);
+        if (FMT == FMT_F16) lvo_last = kpast ? kOobPart : lvo;
+      }
     }
     return __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(wr, vo, so, 2));
   };
@@ -408,9 +416,10 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
   auto step = [&](const u4 v) {
     h2 s2 = (h2){(_Float16)0.f, (_Float16)0.f}, z2 = s2;
     if (FMT != FMT_F16) {
-      const uint32_t e = szl[sa];
-      s2 = as_h2(__builtin_amdgcn_perm(e, e, 0x01000100u));
-      z2 = as_h2(__builtin_amdgcn_perm(e, e, 0x03020302u));
+      // broadcast halves: the packed ops' operand selectors read them in place
+      const h2 e = as_h2(szl[sa]);
+      s2 = __builtin_shufflevector(e, e, 0, 0);
+      z2 = __builtin_shufflevector(e, e, 1, 1);
     }
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
@@ -433,10 +442,18 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
     }
   };
 
+  // wave priority falls with progress (the arbiter issues from the highest
+  // priority ready wave): the waves of a SIMD advance together, so the last
+  // units are not left to one wave that cannot hide the load latency alone
+  __builtin_amdgcn_s_setprio(3);
+  const int q1 = nu >> 2, q2 = nu >> 1, q3 = (3 * nu) >> 2;
   for (int base = 0; base < nu; base += kD) {
 #pragma unroll
     for (int d = 0; d < kD; ++d) {
       if (base + d < nu) {
+        if (base + d == q1) __builtin_amdgcn_s_setprio(2);
+        if (base + d == q2) __builtin_amdgcn_s_setprio(1);
+        if (base + d == q3) __builtin_amdgcn_s_setprio(0);
         step(raw[d]);
         xa += XADV;
         sa += sadv;
