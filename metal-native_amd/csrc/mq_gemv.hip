@@ -210,9 +210,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvKArgs p) {
     const int kin = jl * KSTEP + klane;
     h2 s2 = (h2){(_Float16)0.f, (_Float16)0.f}, z2 = s2;
     if (FMT != FMT_F16) {
-      const uint32_t e = szrow[((kb + kin) >> p.gshift) - g0];
-      s2 = as_h2(__builtin_amdgcn_perm(e, e, 0x01000100u));
-      z2 = as_h2(__builtin_amdgcn_perm(e, e, 0x03020302u));
+      // broadcast halves: the packed ops' operand selectors read them in place
+      const h2 e = as_h2(szrow[((kb + kin) >> p.gshift) - g0]);
+      s2 = __builtin_shufflevector(e, e, 0, 0);
+      z2 = __builtin_shufflevector(e, e, 1, 1);
     }
     const _Float16* xa = xs + xrow + xswz(kin);
 #pragma unroll
