@@ -159,6 +159,19 @@ MQ_API int mq_attention_decode_rope_f16(const void* qkv, const float* cos_table,
                                         int32_t kv_heads, int32_t head_dim, int64_t max_len, float scale,
                                         void* workspace, int64_t workspace_bytes, void* stream);
 
+/* Greedy decode tail in one launch (decoder glue, no reference counterpart;
+ * replaces torch.argmax + the embedding lookup + the position update of a
+ * decode loop): token[0] = argmax(logits[vocab]) in torch.argmax order (NaN
+ * above every number, ties to the lowest index), pos[0] += 1, and x[0:d] =
+ * embed row token (row stride embed_stride elements).  The workspace of
+ * mq_argmax_embed_workspace_size(vocab) bytes starts with a counter that must
+ * be zero before the first call; every call leaves it zero.  Calls sharing a
+ * workspace must be stream-ordered. */
+MQ_API int64_t mq_argmax_embed_workspace_size(int64_t vocab);
+MQ_API int mq_argmax_embed_f16(const void* logits, int64_t vocab, const void* embed, int64_t embed_stride, int64_t d,
+                               int64_t* token, int64_t* pos, void* x, void* workspace, int64_t workspace_bytes,
+                               void* stream);
+
 /* Kernel-path override and layout knobs for tests and tuning (no reference
  * counterpart).  Keys: "force_path" (0 automatic, 2 tiled MFMA GEMM,
  * 3 generic, 6 decode GEMV), "gemv_steps" (K steps per wavefront of the

@@ -399,6 +399,26 @@ MQ_API int mq_attention_decode_rope_f16(const void* qkv, const float* cos_table,
   return MQ_SUCCESS;
 }
 
+MQ_API int64_t mq_argmax_embed_workspace_size(int64_t vocab) {
+  if (vocab < 1 || vocab > (int64_t)INT32_MAX - 2048) return -1;
+  return (int64_t)mq::argmax_embed_workspace(vocab);
+}
+
+MQ_API int mq_argmax_embed_f16(const void* logits, int64_t vocab, const void* embed, int64_t embed_stride, int64_t d,
+                               int64_t* token, int64_t* pos, void* x, void* workspace, int64_t workspace_bytes,
+                               void* stream) {
+  if (!logits || !embed || !token || !pos || !x || !workspace)
+    return fail(MQ_INVALID_ARGUMENT, "argmax_embed: null pointer argument");
+  if (vocab < 1 || vocab > (int64_t)INT32_MAX - 2048 || d < 1 || d > INT32_MAX || embed_stride < d)
+    return fail(MQ_INVALID_ARGUMENT, "argmax_embed: bad shape");
+  if (workspace_bytes < (int64_t)mq::argmax_embed_workspace(vocab))
+    return fail(MQ_INVALID_ARGUMENT, "argmax_embed: workspace too small");
+  hipError_t e = mq::argmax_embed_launch(logits, vocab, embed, embed_stride, (int)d, token, pos, x, workspace,
+                                         (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "argmax_embed: kernel launch failed");
+  return MQ_SUCCESS;
+}
+
 MQ_API int mq_set_option(const char* key, int64_t value) {
   if (!key) return fail(MQ_INVALID_ARGUMENT, "set_option: null key");
   if (std::strcmp(key, "force_path") == 0) {

@@ -402,6 +402,86 @@ __global__ __launch_bounds__(64) void attn_fused_d_kernel(const _Float16* qkv, c
   if (lane == 0) __hip_atomic_store(cnt + h, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
+// ---- greedy decode tail: token = argmax(logits), pos += 1, x = embed[token] ----
+// torch.argmax order: NaN above every number, ties to the lowest index.
+__device__ __forceinline__ bool am_better(float v1, int i1, float v2, int i2) {
+  const bool n1 = v1 != v1, n2 = v2 != v2;
+  if (n1 != n2) return n1;
+  if (!n1 && v1 != v2) return v1 > v2;
+  return i1 < i2;
+}
+__device__ __forceinline__ void am_wave(float& v, int& i) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float v2 = __shfl_xor(v, o);
+    const int i2 = __shfl_xor(i, o);
+    if (am_better(v2, i2, v, i)) { v = v2; i = i2; }
+  }
+}
+// 256 threads x 8 logits per workgroup; the per-workgroup best goes to a
+// record (system-scope stores), and the last workgroup to arrive reduces the
+// records, writes the token and the next position and copies the embedding
+// row, then clears the arrival counter for the next launch.
+__global__ __launch_bounds__(256) void argmax_embed_kernel(const _Float16* logits, int V, const _Float16* embed,
+                                                           int64_t lde, int d, int64_t* tok, int64_t* pos,
+                                                           _Float16* x, float* rv, int* ri, unsigned* cnt) {
+  __shared__ float sv[4];
+  __shared__ int si[4];
+  __shared__ unsigned s_arrived;
+  __shared__ int s_tok;
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int nwg = gridDim.x;
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  const int i0 = (blockIdx.x * 256 + t) * 8;
+  if (i0 + 8 <= V && ((uintptr_t)logits & 15) == 0) {
+    const h8 v = *(const h8*)(logits + i0);
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      if (am_better((float)v[e], i0 + e, bv, bi)) { bv = (float)v[e]; bi = i0 + e; }
+  } else {
+    for (int e = 0; e < 8 && i0 + e < V; ++e) {
+      const float f = (float)logits[i0 + e];
+      if (am_better(f, i0 + e, bv, bi)) { bv = f; bi = i0 + e; }
+    }
+  }
+  am_wave(bv, bi);
+  if (lane == 0) { sv[w] = bv; si[w] = bi; }
+  __syncthreads();
+  if (t == 0) {
+    for (int k = 1; k < 4; ++k)
+      if (am_better(sv[k], si[k], bv, bi)) { bv = sv[k]; bi = si[k]; }
+    __hip_atomic_store(rv + blockIdx.x, bv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    __hip_atomic_store(ri + blockIdx.x, bi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    // the record stores have completed before the arrival is counted
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    s_arrived = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  }
+  __syncthreads();
+  if (s_arrived != (unsigned)(nwg - 1)) return;
+  bv = -INFINITY;
+  bi = 0x7fffffff;
+  for (int k = t; k < nwg; k += 256) {
+    const float v2 = __hip_atomic_load(rv + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    const int i2 = __hip_atomic_load(ri + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    if (am_better(v2, i2, bv, bi)) { bv = v2; bi = i2; }
+  }
+  am_wave(bv, bi);
+  if (lane == 0) { sv[w] = bv; si[w] = bi; }
+  __syncthreads();
+  if (t == 0) {
+    for (int k = 1; k < 4; ++k)
+      if (am_better(sv[k], si[k], bv, bi)) { bv = sv[k]; bi = si[k]; }
+    s_tok = bi;
+    tok[0] = bi;
+    pos[0] = pos[0] + 1;
+    __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  }
+  __syncthreads();
+  const _Float16* row = embed + (int64_t)s_tok * lde;
+  for (int k = t; k < d; k += 256) x[k] = row[k];
+}
+
 }  // namespace
 
 hipError_t add_rmsnorm_launch(void* x, const void* delta, const void* w, void* out, int rows, int n, float eps,
@@ -474,6 +554,22 @@ hipError_t attn_fused_launch(const void* qkv, const float* cos_t, const float* s
                        pos, (_Float16*)kc, (_Float16*)vc, (_Float16*)out, rec, cnt, H, KVH, L, scale);
   else
     return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+size_t argmax_embed_workspace(int64_t V) {
+  const int64_t nwg = (V + 2047) / 2048;
+  return 256 + 8 * (size_t)nwg;   // counter (256-byte aligned), then values and indices
+}
+
+hipError_t argmax_embed_launch(const void* logits, int64_t V, const void* embed, int64_t lde, int d, int64_t* tok,
+                               int64_t* pos, void* x, void* ws, hipStream_t s) {
+  const int nwg = (int)((V + 2047) / 2048);
+  unsigned* cnt = (unsigned*)ws;
+  float* rv = (float*)((unsigned char*)ws + 256);
+  int* ri = (int*)(rv + nwg);
+  hipLaunchKernelGGL(argmax_embed_kernel, dim3(nwg), dim3(256), 0, s, (const _Float16*)logits, (int)V,
+                     (const _Float16*)embed, lde, d, tok, pos, (_Float16*)x, rv, ri, cnt);
   return hipGetLastError();
 }
 

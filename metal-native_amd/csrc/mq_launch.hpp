@@ -116,6 +116,13 @@ hipError_t attn_fused_launch(const void* qkv, const float* cos_t, const float* s
 hipError_t attn_decode_launch(const void* q, const void* kc, const void* vc, const int64_t* pos, void* out, int H,
                               int KVH, int D, int64_t L, float scale, void* ws, hipStream_t s);
 
+// greedy decode tail: tok = argmax(logits[V]) (torch.argmax order), pos += 1,
+// x[d] = embed row tok (row stride lde); ws: argmax_embed_workspace bytes whose
+// leading counter is zero (every launch leaves it zero)
+size_t argmax_embed_workspace(int64_t V);
+hipError_t argmax_embed_launch(const void* logits, int64_t V, const void* embed, int64_t lde, int d, int64_t* tok,
+                               int64_t* pos, void* x, void* ws, hipStream_t s);
+
 hipError_t swiglu_launch(const void* gate, const void* up, void* out, int64_t n, hipStream_t s);
 
 // fp16 GEMV with B stored [K, N] (transpose_b == false): C = A . B.

@@ -59,6 +59,9 @@ SIGNATURES = {
                                             _c_void_p]),
     "mq_attention_decode_f16": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i32, _i32, _i32,
                                        _i64, ctypes.c_float, _c_void_p, _i64, _c_void_p]),
+    "mq_argmax_embed_workspace_size": (_i64, [_i64]),
+    "mq_argmax_embed_f16": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _i64, _c_void_p, _c_void_p, _c_void_p,
+                                   _c_void_p, _i64, _c_void_p]),
     "mq_set_option": (_i32, [ctypes.c_char_p, _i64]),
     "mq_last_path": (_i32, []),
     "mq_last_error": (ctypes.c_char_p, []),

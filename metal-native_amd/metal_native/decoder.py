@@ -15,7 +15,9 @@ projection is an int4 g128 ``dequant_matmul``:
 Residual add + RMSNorm runs inside the following GEMV (the row-block
 kernel's staging), rotary embedding + KV-cache write + single-token
 grouped-query attention is one glue kernel (mq_glue.hip); the
-embedding lookup and the greedy argmax are PyTorch ops on the same stream.
+embedding lookup and the greedy argmax are PyTorch ops on the same stream in
+``step``; ``step_chain`` (the timed decode loop) replaces them with one fused
+argmax + next-position + embedding-lookup kernel.
 The decode step has static shapes (the position is a device tensor), so a
 whole step is captured in a HIP graph and replayed token after token.
 ``reference_step`` restates the step in plain fp32 PyTorch for the tests.
@@ -140,9 +142,13 @@ class SyntheticDecoder:
         self.resid = torch.zeros((2, 1, d), dtype=torch.float16, device=self.device)
         # fused rotary + attention workspace (per-head counters start at zero)
         self.attn_ws = ops.attention_decode_rope_workspace(cfg.heads, cfg.head_dim, cfg.max_len, self.device)
+        # greedy decode chain: the next step's embedding row and the tail workspace
+        self.x0 = torch.zeros((1, d), dtype=torch.float16, device=self.device)
+        self.tail_ws = ops.argmax_embed_workspace(cfg.vocab, self.device)
 
     # one decode step: token [1] int64, pos [1] int64 (device tensors) -> next token [1]
-    def step(self, token: torch.Tensor, pos: torch.Tensor, return_logits: bool = False):
+    def step(self, token: torch.Tensor, pos: torch.Tensor, return_logits: bool = False,
+             x_in: torch.Tensor | None = None):
         """Five launches per layer: QKV with the residual add + RMSNorm fused
         into it (+bias), RoPE + cache write + attention (one kernel), o_proj,
         gate/up with the residual add + RMSNorm fused (+SwiGLU), down.  The
@@ -151,7 +157,7 @@ class SyntheticDecoder:
         cfg = self.cfg
         H, KVH, Dh = cfg.heads, cfg.kv_heads, cfg.head_dim
         scale = 1.0 / math.sqrt(Dh)
-        x = self.embed.index_select(0, token)                      # [1, d] residual stream
+        x = self.embed.index_select(0, token) if x_in is None else x_in   # [1, d] residual stream
         bufs = (self.resid[0], self.resid[1])
         cur = 0
         delta = None
@@ -168,8 +174,22 @@ class SyntheticDecoder:
             cur ^= 1
             delta = L["down"](act)
         logits = ops.rmsnorm_dequant_matmul(x, delta, self.norm, cfg.eps, bufs[cur], *self.lm_head.operands())
+        if x_in is not None:
+            return logits
         nxt = torch.argmax(logits.float(), dim=-1)
         return (nxt, logits) if return_logits else nxt
+
+    def start_chain(self, token: torch.Tensor) -> None:
+        """Stage the embedding row of ``token`` for ``step_chain``."""
+        self.x0.copy_(self.embed.index_select(0, token))
+
+    def step_chain(self, token: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
+        """One greedy step fed by the staged row ``x0``; in place afterwards:
+        ``token`` = the next token, ``pos`` + 1 and ``x0`` = its embedding row
+        (one fused argmax + lookup kernel).  Returns the logits."""
+        logits = self.step(token, pos, x_in=self.x0)
+        ops.argmax_embed(logits, self.embed, token, pos, self.x0, self.tail_ws)
+        return logits
 
     def reference_step(self, token: int, pos: int, dequant) -> torch.Tensor:
         """The same step in fp32 torch with weights from ``dequant(qlinear) ->
@@ -216,12 +236,12 @@ def decode_tokens_per_second(model: SyntheticDecoder, n_tokens: int = 64, warmup
     with torch.cuda.stream(stream):
         for _ in range(warmup):  # eager warm-up: kernels loaded, workspaces allocated
             model.step(tok, pos)
+        model.start_chain(tok)
+        model.step_chain(tok, pos)   # eager warm-up of the chained step
     torch.cuda.synchronize(dev)
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=stream):
-        nxt = model.step(tok, pos)
-        tok.copy_(nxt)
-        pos.add_(1)
+        model.step_chain(tok, pos)   # next token, position and embedding row updated in place
     pos.fill_(model.prefilled)
     graph.replay()  # one untimed replay
     pos.fill_(model.prefilled)

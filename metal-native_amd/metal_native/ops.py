@@ -461,6 +461,36 @@ def attention_decode_rope(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tenso
     return out
 
 
+def argmax_embed_workspace(vocab: int, device) -> torch.Tensor:
+    """Zeroed workspace for ``argmax_embed``; keep one per stream."""
+    nb = _L.mq_argmax_embed_workspace_size(int(vocab))
+    if nb < 0:
+        raise MetalNativeError(f"argmax_embed: vocabulary size {vocab} not supported")
+    return torch.zeros(nb, dtype=torch.uint8, device=device)
+
+
+def argmax_embed(logits: torch.Tensor, embed: torch.Tensor, token: torch.Tensor, pos: torch.Tensor,
+                 x: torch.Tensor, workspace: torch.Tensor) -> None:
+    """Greedy decode tail in one launch, in place: ``token[0] =
+    argmax(logits)`` (torch.argmax order: NaN above every number, ties to
+    the lowest index), ``pos[0] += 1`` and ``x[0] = embed[token]``."""
+    V = logits.numel()
+    d = embed.shape[1]
+    if logits.dtype != torch.float16 or embed.dtype != torch.float16 or x.dtype != torch.float16:
+        raise MetalNativeError("argmax_embed: logits, embed and x must be Float16")
+    if token.dtype != torch.int64 or pos.dtype != torch.int64 or token.numel() < 1 or pos.numel() < 1:
+        raise MetalNativeError("argmax_embed: token and pos must be Int64 with one element")
+    if not logits.is_contiguous() or embed.stride(1) != 1 or not x.is_contiguous() or x.numel() < d:
+        raise MetalNativeError("argmax_embed: contiguous logits and x, embed rows with unit stride")
+    if embed.shape[0] != V:
+        raise MetalNativeError("argmax_embed: embed must have one row per logit")
+    for t in (logits, embed, token, pos, x, workspace):
+        if t.device != logits.device or t.device.type != "cuda":
+            raise MetalNativeError("argmax_embed: all tensors must be on the same GPU")
+    _check(_L.mq_argmax_embed_f16(_ptr(logits), V, _ptr(embed), embed.stride(0), d, _ptr(token), _ptr(pos), _ptr(x),
+                                  _ptr(workspace), workspace.numel(), _stream_handle(logits.device)))
+
+
 def synchronize() -> None:
     """``_C.synchronize``: wait for all queued GPU work."""
     torch.cuda.synchronize()

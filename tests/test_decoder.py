@@ -79,3 +79,41 @@ def test_graph_replay_matches_eager(gpu):
         return out
 
     assert run(False) == run(True)
+
+
+def test_chained_graph_matches_eager(gpu):
+    """The timed decode loop: step_chain (fused argmax + position + embedding
+    row) captured once and replayed gives the eager steps' tokens."""
+    from metal_native.decoder import SyntheticDecoder
+
+    m = SyntheticDecoder(tiny(), gpu, seed=5, prefilled=8)
+    tok = torch.tensor([3], device=gpu)
+    pos = torch.tensor([8], device=gpu)
+    want = []
+    for _ in range(6):
+        tok = m.step(tok, pos)
+        pos = pos + 1
+        want.append(int(tok.item()))
+    m = SyntheticDecoder(tiny(), gpu, seed=5, prefilled=8)
+    tok = torch.tensor([3], device=gpu)
+    pos = torch.tensor([8], device=gpu)
+    s = torch.cuda.Stream(gpu)
+    s.wait_stream(torch.cuda.current_stream(gpu))
+    with torch.cuda.stream(s):
+        m.start_chain(tok)
+        m.step_chain(tok, pos)   # warm-up: writes cache slot 8, rewritten below
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        m.step_chain(tok, pos)
+    tok.fill_(3)
+    pos.fill_(8)
+    m.start_chain(tok)
+    got = []
+    for _ in range(6):
+        g.replay()
+        torch.cuda.synchronize()  # eager host work between replays
+        got.append(int(tok.item()))
+    assert int(pos.item()) == 14
+    assert got == want
+

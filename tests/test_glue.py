@@ -149,3 +149,37 @@ def test_rmsnorm_fused_into_gemv(gpu, N, K, epi, with_delta):
     assert torch.equal(r1, r2)
     err = (y1.float() - y2.float()).abs()
     assert float(err.max()) <= 2e-2 + 2e-3 * float(y2.float().abs().max()), float(err.max())
+
+
+@pytest.mark.parametrize("V,case", [(152064, "random"), (152064, "tie"), (5001, "nan"), (1000, "neginf"),
+                                    (2048, "tie_last")])
+def test_argmax_embed(gpu, V, case):
+    """One fused launch: token = torch.argmax(logits) (NaN wins, ties go to the
+    lowest index), pos + 1, x = embed row token; twice in a row, so the
+    arrival counter left by the first call is exercised."""
+    from metal_native import ops
+
+    g = torch.Generator(device=gpu)
+    g.manual_seed(V)
+    d = 136
+    embed = torch.randn((V, d), device=gpu, generator=g).half()
+    ws = ops.argmax_embed_workspace(V, gpu)
+    tok = torch.zeros(1, dtype=torch.int64, device=gpu)
+    pos = torch.tensor([41], dtype=torch.int64, device=gpu)
+    x = torch.empty((1, d), dtype=torch.float16, device=gpu)
+    for rep in range(2):
+        logits = torch.randn(V, device=gpu, generator=g).half()
+        if case == "tie":
+            logits[[777, 99999, 150000]] = 60.0
+        elif case == "tie_last":
+            logits[[2046, 2047]] = 60.0
+        elif case == "nan":
+            logits[[4000, 17]] = float("nan")
+        elif case == "neginf":
+            logits.fill_(float("-inf"))
+        want = int(torch.argmax(logits.float()).item())
+        ops.argmax_embed(logits, embed, tok, pos, x, ws)
+        torch.cuda.synchronize()
+        assert int(tok.item()) == want
+        assert int(pos.item()) == 42 + rep
+        assert torch.equal(x[0], embed[want])
