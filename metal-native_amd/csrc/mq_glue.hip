@@ -288,11 +288,21 @@ __global__ __launch_bounds__(64) void attn_fused_d_kernel(const _Float16* qkv, c
                                                            int KVH, int64_t L, float scale) {
   __shared__ float qs[D];
   __shared__ float knew[D], vnew[D];
-  __shared__ float pv[kSplit * (D + 1)];
+  __shared__ __align__(16) _Float16 vs[kSplit * D];   // the split's V rows (fp16), position-major
+  __shared__ float ps[kSplit];
   __shared__ float wgt[64];
   __shared__ unsigned int s_arrived;
   const int c = blockIdx.x, h = blockIdx.y, lane = threadIdx.x, nsplit = gridDim.x;
   const int grp = H / KVH, kvh = h / grp;
+  // K and V rows of this lane's position first: they do not depend on pos
+  // (positions past it, or past the cache's end, are loaded and masked)
+  const int t = c * kSplit + lane;
+  const int64_t row = ((int64_t)kvh * L + min((int64_t)t, L - 1)) * D;
+  h8 kv[D / 8], vv[D / 8];
+#pragma unroll
+  for (int j = 0; j < D / 8; ++j) kv[j] = *(const h8*)(kc + row + 8 * j);
+#pragma unroll
+  for (int j = 0; j < D / 8; ++j) vv[j] = *(const h8*)(vc + row + 8 * j);
   const int64_t pos = *pos_p;
   const int n = (int)pos + 1;
   const int t0 = c * kSplit;
@@ -311,14 +321,7 @@ __global__ __launch_bounds__(64) void attn_fused_d_kernel(const _Float16* qkv, c
     if (lane == 0) { put(rec, -INFINITY); put(rec + 1, 0.f); }
     for (int j = lane; j < D; j += 64) put(rec + 2 + j, 0.f);
   } else {
-    const int t = t0 + lane;
     const bool mine = pos >= t0 && pos < t0 + kSplit;   // this split holds the new token
-    const int64_t row = ((int64_t)kvh * L + min((int64_t)t, L - 1)) * D;
-    h8 kv[D / 8], vv[D / 8];
-#pragma unroll
-    for (int j = 0; j < D / 8; ++j) kv[j] = *(const h8*)(kc + row + 8 * j);
-#pragma unroll
-    for (int j = 0; j < D / 8; ++j) vv[j] = *(const h8*)(vc + row + 8 * j);
     const _Float16* qrow = qkv + h * D;
     const _Float16* krow = qkv + (H + kvh) * D;
     const _Float16* vsrc = qkv + (H + KVH + kvh) * D;
@@ -349,20 +352,40 @@ __global__ __launch_bounds__(64) void attn_fused_d_kernel(const _Float16* qkv, c
     const float m = wave_max(sc);
     const float p = t < n ? expf(sc - m) : 0.f;
     const float l = wave_sum(p);
+    // p.V: the V rows go to LDS as fp16 (the new token's is vnew, an fp16
+    // value), then each lane sums its columns over the positions in order
+    ps[lane] = p;
     if (mine && t == pos) {
-      for (int j = 0; j < D; ++j) pv[lane * (D + 1) + j] = p * vnew[j];
+#pragma unroll
+      for (int j = 0; j < D / 8; ++j) {
+        h8 r;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) r[e] = (_Float16)vnew[8 * j + e];
+        *(h8*)(vs + lane * D + 8 * j) = r;
+      }
     } else {
 #pragma unroll
-      for (int j = 0; j < D / 8; ++j)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) pv[lane * (D + 1) + 8 * j + e] = p * (float)vv[j][e];
+      for (int j = 0; j < D / 8; ++j) *(h8*)(vs + lane * D + 8 * j) = vv[j];
     }
     __syncthreads();
-    for (int col = lane; col < D; col += 64) {
-      float o = 0.f;
+    if (D == 128) {   // lane: columns 2*lane, 2*lane + 1
+      float o0 = 0.f, o1 = 0.f;
 #pragma unroll 16
-      for (int u = 0; u < kSplit; ++u) o += pv[u * (D + 1) + col];
-      put(rec + 2 + col, o);
+      for (int u = 0; u < kSplit; ++u) {
+        const h2 v2 = *(const h2*)(vs + u * D + 2 * lane);
+        const float pu = ps[u];
+        o0 += pu * (float)v2.x;
+        o1 += pu * (float)v2.y;
+      }
+      put(rec + 2 + 2 * lane, o0);
+      put(rec + 3 + 2 * lane, o1);
+    } else {
+      for (int col = lane; col < D; col += 64) {
+        float o = 0.f;
+#pragma unroll 16
+        for (int u = 0; u < kSplit; ++u) o += ps[u] * (float)vs[u * D + col];
+        put(rec + 2 + col, o);
+      }
     }
     if (lane == 0) { put(rec, m); put(rec + 1, l); }
   }
