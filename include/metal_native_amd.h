@@ -148,11 +148,11 @@ MQ_API int mq_attention_decode_f16(const void* q, const void* k_cache, const voi
 
 /* rope_kv + attention_decode in one launch (head_dim 64 or 128, max_len <=
  * 4096): rotates q and the new k from qkv (layout as rope_kv), writes the new
- * k and v into the caches at pos and returns attention_decode's output.  The
- * workspace of mq_attention_decode_rope_workspace_size(heads, head_dim,
- * max_len) bytes (-1: shape not supported) starts with per-head counters that
- * must be zero before the first call (zero it once); every call leaves them
- * zero.  Calls sharing a workspace must be stream-ordered. */
+ * k and v into the caches at pos and returns attention_decode's output (one
+ * workgroup per query head; its waves' partial softmax sums are combined in
+ * LDS).  The workspace of mq_attention_decode_rope_workspace_size(heads,
+ * head_dim, max_len) bytes (-1: shape not supported) is reserved: the current
+ * kernel does not read or write it. */
 MQ_API int64_t mq_attention_decode_rope_workspace_size(int32_t heads, int32_t head_dim, int64_t max_len);
 MQ_API int mq_attention_decode_rope_f16(const void* qkv, const float* cos_table, const float* sin_table,
                                         const int64_t* pos, void* k_cache, void* v_cache, void* out, int32_t heads,

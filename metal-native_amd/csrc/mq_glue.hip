@@ -10,6 +10,11 @@
 
 #include <algorithm>
 
+// Timing probe points; empty unless a benchmark harness defines MQ_GTRACE.
+#ifndef MQ_GTRACE
+#define MQ_GTRACE(slot)
+#endif
+
 namespace mq {
 namespace {
 
@@ -270,159 +275,168 @@ __global__ __launch_bounds__(128) void attn_combine_kernel(const float* ws, _Flo
   }
 }
 
-// Rotary embedding + cache write + attention + split combine in one launch.
-// Workgroup (split c, head h), lane = position, as attn_partial_d_kernel, and:
-//  * q of head h is rotated here, rounded to fp16 as rope_kv stores it;
-//  * the split holding position pos rotates k and takes v of the new token
-//    from qkv and uses them for that position; the workgroup of the first
-//    query head of each KV group writes them into the caches (no other
-//    workgroup reads position pos);
-//  * the split's record (m, l, o[D]) goes out with system-scope stores (the
-//    splits of a head run on different XCDs), then a per-head counter elects
-//    the last workgroup of the head, which combines the splits in split order
-//    and resets the counter (counters start at zero, calls are stream-ordered).
+// Rotary embedding + cache write + attention in one launch, one workgroup per
+// query head.  Wave w takes the 64-position splits w, w + NW, ...; a split's
+// K and V rows are loaded coalesced (LPR = D/8 lanes per row, each lane one
+// 16-byte piece of columns 8q..8q+7, RPI = 64/LPR rows per load), the next
+// split's rows prefetched while the current one computes.  Scores: per-lane
+// partial dot products over the piece, summed across the LPR lanes of a row
+// by recursive halving (LPR - 1 shuffles for LPR rows; lane q of a row group
+// ends with row q's score).  P.V: each lane weights its rows' V pieces and the
+// RPI row groups are summed by shuffles.  A wave keeps a running max / exp-sum
+// / P.V over its splits; wave 0 combines the waves' partials through LDS.
+// q and the new k are rotated and rounded to fp16 as rope_kv stores them; the
+// new token's k and v are taken from registers (its cache row is stale until
+// written) and written into the caches by the workgroup of the first query
+// head of each KV group (no other workgroup reads position pos).
 template <int D>
-__global__ __launch_bounds__(64) void attn_fused_d_kernel(const _Float16* qkv, const float* cos_t, const float* sin_t,
-                                                           const int64_t* pos_p, _Float16* kc, _Float16* vc,
-                                                           _Float16* out, float* ws, unsigned int* cnt, int H,
-                                                           int KVH, int64_t L, float scale) {
+__global__ __launch_bounds__(768) void attn_head_d_kernel(const _Float16* qkv, const float* cos_t, const float* sin_t,
+                                                          const int64_t* pos_p, _Float16* kc, _Float16* vc,
+                                                          _Float16* out, int H, int KVH, int64_t L, float scale) {
+  // floating-point attention (checked against a tolerance, not bit-exact):
+  // multiply-adds may fuse here, unlike in the dequant arithmetic
+#pragma clang fp contract(fast)
+  constexpr int LPR = D / 8;        // lanes per row
+  constexpr int RPI = 64 / LPR;     // rows per load instruction
+  constexpr int NI = 8;             // row loads per step (K and V: 64 VGPRs)
+  constexpr int SUB = NI * RPI;     // positions per step: 32 (D = 128) or 64 (D = 64)
+  constexpr int DUP = LPR / NI;     // lanes left holding the same score after the halving
+  constexpr int HALF = D / 2;
   __shared__ float qs[D];
-  __shared__ float knew[D], vnew[D];
-  __shared__ __align__(16) _Float16 vs[kSplit * D];   // the split's V rows (fp16), position-major
-  __shared__ float ps[kSplit];
-  __shared__ float wgt[64];
-  __shared__ unsigned int s_arrived;
-  const int c = blockIdx.x, h = blockIdx.y, lane = threadIdx.x, nsplit = gridDim.x;
+  __shared__ __align__(16) _Float16 kn16[D], vn16[D];   // the new token's rotated k and its v
+  __shared__ float wm[12], wl[12], wo[12][D];
+  const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int NW = blockDim.x >> 6;
+  const int q = lane % LPR, rg = lane / LPR;   // column piece, row group
+  const int nsplit = (int)((L + SUB - 1) / SUB);   // steps over the cache
   const int grp = H / KVH, kvh = h / grp;
-  // K and V rows of this lane's position first: they do not depend on pos
-  // (positions past it, or past the cache's end, are loaded and masked)
-  const int t = c * kSplit + lane;
-  const int64_t row = ((int64_t)kvh * L + min((int64_t)t, L - 1)) * D;
-  h8 kv[D / 8], vv[D / 8];
+  h8 kv[NI], vv[NI];
+  auto load_rows = [&](int c) {
 #pragma unroll
-  for (int j = 0; j < D / 8; ++j) kv[j] = *(const h8*)(kc + row + 8 * j);
-#pragma unroll
-  for (int j = 0; j < D / 8; ++j) vv[j] = *(const h8*)(vc + row + 8 * j);
+    for (int i = 0; i < NI; ++i) {
+      const int64_t t = min((int64_t)(c * SUB + RPI * i + rg), L - 1);
+      const int64_t off = ((int64_t)kvh * L + t) * D + 8 * q;
+      kv[i] = *(const h8*)(kc + off);
+      vv[i] = *(const h8*)(vc + off);
+    }
+  };
+  load_rows(w);   // NW <= nsplit: every wave has a first split
+  MQ_GTRACE(0);
   const int64_t pos = *pos_p;
   const int n = (int)pos + 1;
-  const int t0 = c * kSplit;
   const float* cs = cos_t + pos * D;
   const float* sn = sin_t + pos * D;
-  constexpr int HALF = D / 2;
   auto rope = [&](const _Float16* src, int j) -> _Float16 {
     const float x = (float)src[j];
     const float pair = (float)src[j < HALF ? j + HALF : j - HALF];
     const float rot = j < HALF ? -pair : pair;
     return (_Float16)(x * cs[j] + rot * sn[j]);
   };
-  float* rec = ws + ((int64_t)h * nsplit + c) * (D + 2);  // [m, l, o[D]]
-  auto put = [&](float* a, float v) { __hip_atomic_store(a, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM); };
-  if (t0 >= n) {
-    if (lane == 0) { put(rec, -INFINITY); put(rec + 1, 0.f); }
-    for (int j = lane; j < D; j += 64) put(rec + 2 + j, 0.f);
-  } else {
-    const bool mine = pos >= t0 && pos < t0 + kSplit;   // this split holds the new token
+  {
     const _Float16* qrow = qkv + h * D;
     const _Float16* krow = qkv + (H + kvh) * D;
     const _Float16* vsrc = qkv + (H + KVH + kvh) * D;
-    for (int j = lane; j < D; j += 64) qs[j] = (float)rope(qrow, j);
-    if (mine) {
-      const int64_t prow = ((int64_t)kvh * L + pos) * D;
-      for (int j = lane; j < D; j += 64) {
-        const _Float16 kn = rope(krow, j), vn = vsrc[j];
-        knew[j] = (float)kn;
-        vnew[j] = (float)vn;
-        if (h % grp == 0) {
-          kc[prow + j] = kn;
-          vc[prow + j] = vn;
-        }
+    const int64_t prow = ((int64_t)kvh * L + pos) * D;
+    for (int j = tid; j < D; j += blockDim.x) {
+      qs[j] = (float)rope(qrow, j);
+      const _Float16 kn = rope(krow, j), vn = vsrc[j];
+      kn16[j] = kn;
+      vn16[j] = vn;
+      if (h % grp == 0) {
+        kc[prow + j] = kn;
+        vc[prow + j] = vn;
       }
     }
-    __syncthreads();
-    float acc = 0.f;
-    if (mine && t == pos) {
-      for (int j = 0; j < D; ++j) acc += qs[j] * knew[j];
-    } else {
+  }
+  __syncthreads();
+  MQ_GTRACE(1);
+  h2 qh[4];   // q is an fp16 value (rounded as rope_kv stores it)
 #pragma unroll
-      for (int j = 0; j < D / 8; ++j)
+  for (int e = 0; e < 4; ++e) qh[e] = (h2){(_Float16)qs[8 * q + 2 * e], (_Float16)qs[8 * q + 2 * e + 1]};
+  float m_run = -INFINITY, l_run = 0.f, o_run[8] = {};
+  for (int c = w; c < nsplit; c += NW) {
+    const int t0 = c * SUB;
+    if (t0 >= n) break;   // this and the wave's later steps lie past the new token
+    if (pos >= t0 && pos < t0 + SUB) {   // the split holding the new token: its row from registers
+      const h8 kn = *(const h8*)(kn16 + 8 * q), vn = *(const h8*)(vn16 + 8 * q);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc += qs[8 * j + e] * (float)kv[j][e];
+      for (int i = 0; i < NI; ++i)
+        if (t0 + RPI * i + rg == pos) { kv[i] = kn; vv[i] = vn; }
     }
-    const float sc = t < n ? acc * scale : -INFINITY;
+    // partial scores of the lane's NI rows (row i: position t0 + RPI*i + rg)
+    float d[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      float a = 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        a = __builtin_amdgcn_fdot2(qh[e], (h2){kv[i][2 * e], kv[i][2 * e + 1]}, a, false);
+      d[i] = a;
+    }
+    // recursive halving across the LPR lanes of the row group (lane q ends
+    // with row q / DUP), then the DUP lanes of a row add theirs
+#pragma unroll
+    for (int b = LPR / 2, S = NI; S > 1; b >>= 1, S >>= 1) {
+      const bool up = (q & b) != 0;
+#pragma unroll
+      for (int k = 0; k < S / 2; ++k) {
+        const float keep = up ? d[k + S / 2] : d[k];
+        const float send = up ? d[k] : d[k + S / 2];
+        d[k] = keep + __shfl_xor(send, b);
+      }
+    }
+#pragma unroll
+    for (int b = DUP / 2; b >= 1; b >>= 1) d[0] += __shfl_xor(d[0], b);
+    const int t = t0 + RPI * (q / DUP) + rg;   // the position whose full score this lane holds
+    const float sc = t < n ? d[0] * scale : -INFINITY;
     const float m = wave_max(sc);
     const float p = t < n ? expf(sc - m) : 0.f;
-    const float l = wave_sum(p);
-    // p.V: the V rows go to LDS as fp16 (the new token's is vnew, an fp16
-    // value), then each lane sums its columns over the positions in order
-    ps[lane] = p;
-    if (mine && t == pos) {
+    const float l = wave_sum(q % DUP == 0 ? p : 0.f);
+    float o[8] = {};
 #pragma unroll
-      for (int j = 0; j < D / 8; ++j) {
-        h8 r;
+    for (int i = 0; i < NI; ++i) {
+      const float pi = __shfl(p, rg * LPR + i * DUP);   // row i of this row group
 #pragma unroll
-        for (int e = 0; e < 8; ++e) r[e] = (_Float16)vnew[8 * j + e];
-        *(h8*)(vs + lane * D + 8 * j) = r;
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < D / 8; ++j) *(h8*)(vs + lane * D + 8 * j) = vv[j];
+      for (int e = 0; e < 8; ++e) o[e] += pi * (float)vv[i][e];
     }
-    __syncthreads();
-    if (D == 128) {   // lane: columns 2*lane, 2*lane + 1
-      float o0 = 0.f, o1 = 0.f;
-#pragma unroll 16
-      for (int u = 0; u < kSplit; ++u) {
-        const h2 v2 = *(const h2*)(vs + u * D + 2 * lane);
-        const float pu = ps[u];
-        o0 += pu * (float)v2.x;
-        o1 += pu * (float)v2.y;
-      }
-      put(rec + 2 + 2 * lane, o0);
-      put(rec + 3 + 2 * lane, o1);
-    } else {
-      for (int col = lane; col < D; col += 64) {
-        float o = 0.f;
-#pragma unroll 16
-        for (int u = 0; u < kSplit; ++u) o += ps[u] * (float)vs[u * D + col];
-        put(rec + 2 + col, o);
-      }
+    // the next split's rows: issued once this split's are consumed (the fence
+    // keeps the loads from being hoisted above the uses, doubling the rows live)
+    asm volatile("" ::: "memory");
+    if (c + NW < nsplit) load_rows(c + NW);
+#pragma unroll
+    for (int b = LPR; b < 64; b <<= 1)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] += __shfl_xor(o[e], b);
+    const float mn = fmaxf(m_run, m);
+    const float a = m_run == -INFINITY ? 0.f : expf(m_run - mn), bsc = expf(m - mn);
+    l_run = l_run * a + l * bsc;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o_run[e] = o_run[e] * a + o[e] * bsc;
+    m_run = mn;
+  }
+  MQ_GTRACE(2);
+  if (lane == 0) { wm[w] = m_run; wl[w] = l_run; }
+  if (rg == 0)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) wo[w][8 * q + e] = o_run[e];
+  __syncthreads();
+  MQ_GTRACE(3);
+  if (w == 0 && rg == 0) {
+    float mm = -INFINITY;
+    for (int ww = 0; ww < NW; ++ww) mm = fmaxf(mm, wm[ww]);
+    float ll = 0.f, o[8] = {};
+    for (int ww = 0; ww < NW; ++ww) {
+      const float f = wm[ww] == -INFINITY ? 0.f : expf(wm[ww] - mm);
+      ll += wl[ww] * f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] += wo[ww][8 * q + e] * f;
     }
-    if (lane == 0) { put(rec, m); put(rec + 1, l); }
+    h8 r;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r[e] = (_Float16)(o[e] / ll);
+    *(h8*)(out + h * D + 8 * q) = r;
   }
-  // every record store has completed before the arrival is counted
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  if (lane == 0) s_arrived = __hip_atomic_fetch_add(cnt + h, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-  __syncthreads();
-  if (s_arrived != (unsigned)(nsplit - 1)) return;
-  // the last workgroup of head h: combine the splits in split order
-  auto get = [&](const float* a) { return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM); };
-  const float* base = ws + (int64_t)h * nsplit * (D + 2);
-  const float mc = lane < nsplit ? get(base + lane * (D + 2)) : -INFINITY;
-  const float lc = lane < nsplit ? get(base + lane * (D + 2) + 1) : 0.f;
-  const float mm = wave_max(mc);
-  const float wc = mc != -INFINITY ? expf(mc - mm) : 0.f;
-  wgt[lane] = wc;   // l and o are summed in split order
-  __syncthreads();
-  float ll = 0.f;
-  for (int cc = 0; cc < nsplit; ++cc) ll += __shfl(lc, cc) * wgt[cc];
-  constexpr int CPL = D / 64;
-  float o[CPL] = {};
-  for (int c0 = 0; c0 < nsplit; c0 += 8) {   // eight splits' loads in flight at a time
-    float v[8][CPL];
-#pragma unroll
-    for (int k = 0; k < 8; ++k)
-#pragma unroll
-      for (int e = 0; e < CPL; ++e)
-        v[k][e] = c0 + k < nsplit ? get(base + (c0 + k) * (D + 2) + 2 + CPL * lane + e) : 0.f;
-#pragma unroll
-    for (int k = 0; k < 8; ++k)
-      if (c0 + k < nsplit)
-#pragma unroll
-        for (int e = 0; e < CPL; ++e) o[e] += v[k][e] * wgt[c0 + k];
-  }
-#pragma unroll
-  for (int e = 0; e < CPL; ++e) out[h * D + CPL * lane + e] = (_Float16)(o[e] / ll);
-  if (lane == 0) __hip_atomic_store(cnt + h, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  MQ_GTRACE(4);
 }
 
 // ---- greedy decode tail: token = argmax(logits), pos += 1, x = embed[token] ----
@@ -554,9 +568,8 @@ hipError_t attn_decode_launch(const void* q, const void* kc, const void* vc, con
   return hipGetLastError();
 }
 
-size_t attn_fused_workspace(int H, int D, int64_t L) {
-  // per-head counters first (256-byte aligned), then the split records
-  return 256 * (((size_t)H * 4 + 255) / 256) + attn_decode_workspace(H, D, L);
+size_t attn_fused_workspace(int, int, int64_t) {
+  return 256;   // reserved: the one-workgroup-per-head kernel combines its splits in LDS
 }
 
 bool attn_fused_supported(int H, int D, int64_t L) {
@@ -566,15 +579,14 @@ bool attn_fused_supported(int H, int D, int64_t L) {
 hipError_t attn_fused_launch(const void* qkv, const float* cos_t, const float* sin_t, const int64_t* pos, void* kc,
                              void* vc, void* out, int H, int KVH, int D, int64_t L, float scale, void* ws,
                              hipStream_t s) {
-  const int nsplit = (int)((L + kSplit - 1) / kSplit);
-  unsigned int* cnt = (unsigned int*)ws;
-  float* rec = (float*)((unsigned char*)ws + 256 * (((size_t)H * 4 + 255) / 256));
+  (void)ws;
+  const int NW = std::min<int64_t>(12, (L + 4095 / D) / (4096 / D));   // one wave per step up to 12
   if (D == 128)
-    hipLaunchKernelGGL(attn_fused_d_kernel<128>, dim3(nsplit, H), dim3(64), 0, s, (const _Float16*)qkv, cos_t, sin_t,
-                       pos, (_Float16*)kc, (_Float16*)vc, (_Float16*)out, rec, cnt, H, KVH, L, scale);
+    hipLaunchKernelGGL(attn_head_d_kernel<128>, dim3(H), dim3(64 * NW), 0, s, (const _Float16*)qkv, cos_t, sin_t,
+                       pos, (_Float16*)kc, (_Float16*)vc, (_Float16*)out, H, KVH, L, scale);
   else if (D == 64)
-    hipLaunchKernelGGL(attn_fused_d_kernel<64>, dim3(nsplit, H), dim3(64), 0, s, (const _Float16*)qkv, cos_t, sin_t,
-                       pos, (_Float16*)kc, (_Float16*)vc, (_Float16*)out, rec, cnt, H, KVH, L, scale);
+    hipLaunchKernelGGL(attn_head_d_kernel<64>, dim3(H), dim3(64 * NW), 0, s, (const _Float16*)qkv, cos_t, sin_t,
+                       pos, (_Float16*)kc, (_Float16*)vc, (_Float16*)out, H, KVH, L, scale);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();

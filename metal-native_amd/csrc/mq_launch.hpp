@@ -105,9 +105,9 @@ hipError_t add_rmsnorm_launch(void* x, const void* delta, const void* w, void* o
 hipError_t rope_kv_launch(const void* qkv, const float* cos_t, const float* sin_t, const int64_t* pos, void* q_out,
                           void* kc, void* vc, int H, int KVH, int D, int64_t L, hipStream_t s);
 size_t attn_decode_workspace(int H, int D, int64_t L);
-// rotary + cache write + attention + split combine in one launch (head_dim 64
-// or 128, at most 64 splits of 64 positions); ws: attn_fused_workspace bytes
-// whose leading per-head counters are zero (every launch leaves them zero)
+// rotary + cache write + attention in one launch, one workgroup per query head
+// (head_dim 64 or 128, L <= 4096); ws: attn_fused_workspace bytes, reserved
+// (the kernel does not touch it)
 size_t attn_fused_workspace(int H, int D, int64_t L);
 bool attn_fused_supported(int H, int D, int64_t L);
 hipError_t attn_fused_launch(const void* qkv, const float* cos_t, const float* sin_t, const int64_t* pos, void* kc,

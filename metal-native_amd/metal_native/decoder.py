@@ -140,7 +140,7 @@ class SyntheticDecoder:
         self.positions = torch.arange(cfg.max_len, device=self.device)
         # two residual-stream buffers (the fused norm + GEMV writes out of place)
         self.resid = torch.zeros((2, 1, d), dtype=torch.float16, device=self.device)
-        # fused rotary + attention workspace (per-head counters start at zero)
+        # fused rotary + attention workspace (reserved by the current kernel)
         self.attn_ws = ops.attention_decode_rope_workspace(cfg.heads, cfg.head_dim, cfg.max_len, self.device)
         # greedy decode chain: the next step's embedding row and the tail workspace
         self.x0 = torch.zeros((1, d), dtype=torch.float16, device=self.device)
