@@ -178,6 +178,8 @@ MQ_API int mq_argmax_embed_f16(const void* logits, int64_t vocab, const void* em
  * decode GEMV, 1..8, 0 automatic), "gemv_tiles_per_wg" (row tiles per
  * workgroup: 1, 2 or 4, 0 automatic), "gemm_prefetch" (K-tiles the prefill GEMM loads
  * ahead: 2, 4 or 8), "gemm_waves" (wavefronts per 128-row GEMM tile: 4 or 8),
+ * "gemm_impl" (prefill GEMM kernel: 0 the register-operand kernel where it applies,
+ * 1 always the LDS-staged kernel; both compute the same contract),
  * force_path 7 selects the row-block decode GEMV.  A layout the decode GEMV cannot stage
  * makes it unavailable (the call then takes the tiled or generic kernel).
  * Returns MQ_INVALID_ARGUMENT for an unknown key or value. */

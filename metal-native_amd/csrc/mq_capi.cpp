@@ -109,11 +109,11 @@ int choose_path(const mq::LinearArgs& a) {
   int forced = g_force_path.load();
   if (forced == PATH_ROWS && rows_ok(a)) return PATH_ROWS;
   if (forced == PATH_DECODE && decode_ok(a)) return PATH_DECODE;
-  if (forced == PATH_TILED && (mq::gemm_supported(a) || mq::tiled_supported(a))) return PATH_TILED;
+  if (forced == PATH_TILED && (mq::gemmr_supported(a) || mq::gemm_supported(a) || mq::tiled_supported(a))) return PATH_TILED;
   if (forced == PATH_GENERIC) return PATH_GENERIC;
   if (rows_ok(a)) return PATH_ROWS;
   if (decode_ok(a)) return PATH_DECODE;
-  if (mq::gemm_supported(a) || mq::tiled_supported(a)) return PATH_TILED;
+  if (mq::gemmr_supported(a) || mq::gemm_supported(a) || mq::tiled_supported(a)) return PATH_TILED;
   return PATH_GENERIC;
 }
 
@@ -132,7 +132,10 @@ int run_linear(const mq::LinearArgs& a, hipStream_t s) {
     if (e != hipSuccess) return hip_fail(e, "dequant_matmul: workspace allocation failed");
     e = mq::gemv_launch(a, pl, ws, s);
   } else if (path == PATH_TILED) {
-    e = mq::gemm_supported(a) ? mq::gemm_launch(a, s) : mq::tiled_launch(a, s);
+    if (mq::g_gemm_impl == 0 && mq::gemmr_supported(a))
+      e = mq::gemmr_launch(a, s);
+    else
+      e = mq::gemm_supported(a) ? mq::gemm_launch(a, s) : mq::tiled_launch(a, s);
   } else {
     e = mq::generic_linear_launch(a, s);
   }
@@ -432,6 +435,11 @@ MQ_API int mq_set_option(const char* key, int64_t value) {
     if (value != 2 && value != 4 && value != 8)
       return fail(MQ_INVALID_ARGUMENT, "set_option: gemm_prefetch must be 2, 4 or 8");
     mq::g_gemm_pf = (int)value;
+    return MQ_SUCCESS;
+  }
+  if (std::strcmp(key, "gemm_impl") == 0) {
+    if (value != 0 && value != 1) return fail(MQ_INVALID_ARGUMENT, "set_option: gemm_impl must be 0 or 1");
+    mq::g_gemm_impl = (int)value;
     return MQ_SUCCESS;
   }
   if (std::strcmp(key, "gemm_waves") == 0) {

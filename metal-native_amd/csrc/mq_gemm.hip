@@ -37,6 +37,7 @@
 namespace mq {
 int g_gemm_pf = 4;
 int g_gemm_waves = 8;
+int g_gemm_impl = 0;
 namespace {
 
 constexpr int BN = 128, BK = MQ_GEMM_BK;

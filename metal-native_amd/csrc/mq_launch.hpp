@@ -69,6 +69,10 @@ hipError_t rows_launch(const LinearArgs& a, const RowsPlan& p, hipStream_t s);
 extern int g_gemm_pf;     // K-tiles in flight ahead of the MFMAs (2, 4 or 8)
 extern int g_gemm_waves;  // wavefronts per workgroup for 128-row tiles (4 or 8)
 bool gemm_supported(const LinearArgs& a);
+// register-B GEMM (weights dequantized into MFMA operands, activations via LDS)
+extern int g_gemm_impl;  // 0: register-B kernel where supported, 1: LDS-staged kernel
+bool gemmr_supported(const LinearArgs& a);
+hipError_t gemmr_launch(const LinearArgs& a, hipStream_t s);
 hipError_t gemm_launch(const LinearArgs& a, hipStream_t s);
 
 // 16x16x32 MFMA GEMM, K steps of 32 (fallback for shapes the GEMM above does not take).

@@ -559,3 +559,36 @@ def test_rows_kernel_ragged_runs(mn, gpu, M, K, N, g, qt, epi):
         check_close(y, acc + b.astype(np.float32), "rows ragged bias")
     else:
         check_close(y, acc, "rows ragged")
+
+
+@pytest.mark.parametrize("impl", [0, 1])
+@pytest.mark.parametrize("qt,epi", [("int4", None), ("int4", "bias"), ("int4", "swiglu"),
+                                    ("int8", None), ("int8", "swiglu")])
+@pytest.mark.parametrize("M,K,N", [(17, 256, 96), (100, 512, 320), (200, 1024, 256), (512, 768, 1056)])
+def test_prefill_gemm_kernels(mn, gpu, impl, qt, epi, M, K, N):
+    """Both prefill GEMM kernels (register-B, impl 0; LDS-staged, impl 1) on
+    ragged M / N tails, int4 g128 and int8 per-channel, each epilogue."""
+    say(f"gemm impl={impl} {qt} {epi} M={M} K={K} N={N}")
+    if qt == "int4":
+        x, wp, s, z = O.make_int4_problem(M, K, N, 128, seed=M + K + N)
+        g = 128
+        acc = O.matmul_f32acc(x, O.dequant_int4(wp, s, z, K, g))
+    else:
+        x, wp, s, z, g = O.make_int8_problem(M, K, N, seed=M + K + N)
+        acc = O.matmul_f32acc(x, O.dequant_int8(wp, s, z, K, g))
+    kw = {}
+    if epi == "bias":
+        b = np.random.default_rng(N).standard_normal(N).astype(np.float16)
+        kw = {"epilogue": "bias", "bias": dev(b, gpu)}
+    elif epi == "swiglu":
+        kw = {"epilogue": "swiglu"}
+    mn.set_option("gemm_impl", impl)
+    try:
+        y, taken = run_dm(mn, gpu, x, wp, s, z, g, qt, "tiled", **kw)
+    finally:
+        mn.set_option("gemm_impl", 0)
+    assert taken == "tiled"
+    if epi == "swiglu":
+        check_swiglu(y, acc, f"gemm impl={impl}")
+    else:
+        check_close(y, acc + b.astype(np.float32) if epi == "bias" else acc, f"gemm impl={impl}")
