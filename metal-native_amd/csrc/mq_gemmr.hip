@@ -25,7 +25,8 @@
 //    waits overlap the other's MFMAs, and no weight is dequantized twice.  The
 //    two partial sums are added once, through LDS, after the K loop.  With one
 //    wave per slice (and one wave per SIMD) the same kernel took 47 us at the
-//    Llama-3.2-3B QKV shape (M = 512) against 35 us with two.
+//    Llama-3.2-3B QKV shape (M = 512) against 35 us with two; a four-way
+//    split (KS = 4, four waves per SIMD, 8-byte int4 loads) took 44 us.
 //  * Global loads run PF K-tiles ahead in a register ring; the next tile's
 //    weights are dequantized while this tile's MFMAs run.
 //  * Workgroups sharing a weight slice (same N block, all M blocks) are placed
@@ -69,8 +70,10 @@ __global__ __launch_bounds__(64 * NW * KS) void gemmr_kernel(GemmRArgs p) {
   constexpr int MB = BM / 32;                          // A blocks per wave
   constexpr int NBB = EPI == EPI_SWIGLU ? 2 : 1;       // B blocks per wave
   constexpr int APT = BM * BK / 8 / NT;                // 16-byte activation pieces per thread per K-tile
-  constexpr int WL = (FMT == FMT_INT4 ? 2 : 4) / KS;   // 16-byte weight loads per B block per K-tile and wave
   constexpr int KKW = 8 / KS;                          // k-steps per wave per K-tile
+  constexpr int NDW = FMT == FMT_INT4 ? KKW : 2 * KKW; // weight dwords per lane per B block per K-tile
+  constexpr int WL = NDW / 4;                          // 16-byte weight loads per lane (0: one 8-byte load)
+  static_assert(KS == 2 || KS == 4, "k split");
   constexpr int WROW = FMT == FMT_INT4 ? BK / 2 : BK;  // weight bytes per row per K-tile
   static_assert(APT >= 1, "tile too small");
   __shared__ __align__(16) _Float16 lds_a0[BM * LDSW];
@@ -117,13 +120,17 @@ __global__ __launch_bounds__(64 * NW * KS) void gemmr_kernel(GemmRArgs p) {
       ok = col < p.N;
       grow = col;
     }
-    woff[j] = ok ? (uint32_t)(grow * p.ldw) + ks * WL * 32 + h * 16 : kOob;
+    // first byte of this lane's k-steps ks*KKW .. : int4 k-step kk sits at
+    // (kk/4)*32 + h*16 + (kk%4)*4, int8 at (kk/2)*32 + h*16 + (kk%2)*8
+    const int kk0 = ks * KKW;
+    const int b0 = FMT == FMT_INT4 ? (kk0 >> 2) * 32 + (kk0 & 3) * 4 : (kk0 >> 1) * 32;
+    woff[j] = ok ? (uint32_t)(grow * p.ldw) + b0 + h * 16 : kOob;
     soff[j] = ok ? (uint32_t)(grow * p.G) * 2 : kOob;
   }
 
   struct Stage {
     u4 a[APT];
-    u4 w[NBB][WL];
+    uint32_t w[NBB][NDW];
     uint16_t s[NBB], z[NBB];
   };
   const int KT = p.K / BK;
@@ -137,7 +144,14 @@ __global__ __launch_bounds__(64 * NW * KS) void gemmr_kernel(GemmRArgs p) {
       const bool wok = ok && woff[j] != kOob;
       const uint32_t wo = woff[j] + kt * WROW;
 #pragma unroll
-      for (int e = 0; e < WL; ++e) st.w[j][e] = bload16_nt(wr, wok ? wo + 32 * e : kOob);
+      for (int e = 0; e < WL; ++e) {
+        const u4 v = bload16_nt(wr, wok ? wo + 32 * e : kOob);
+        st.w[j][4 * e] = v.x; st.w[j][4 * e + 1] = v.y; st.w[j][4 * e + 2] = v.z; st.w[j][4 * e + 3] = v.w;
+      }
+      if constexpr (WL == 0) {
+        const uint64_t v = bload8_nt(wr, wok ? wo : kOob);
+        st.w[j][0] = (uint32_t)v; st.w[j][1] = (uint32_t)(v >> 32);
+      }
       const uint32_t so = wok ? soff[j] + g2 : kOob;
       st.s[j] = bload2h(sr, so);
       st.z[j] = bload2h(zr, so);
@@ -164,24 +178,16 @@ __global__ __launch_bounds__(64 * NW * KS) void gemmr_kernel(GemmRArgs p) {
       const h2 s2 = as_h2((uint32_t)st.s[j] * 0x10001u);
       const h2 z2 = as_h2((uint32_t)st.z[j] * 0x10001u);
 #pragma unroll
-      for (int e = 0; e < WL; ++e) {
-        const u4 v = st.w[j][e];
+      for (int t = 0; t < KKW; ++t) {
         if (FMT == FMT_INT4) {
-          bq[4 * e + 0][j] = dq_int4_dword_perm(v.x, s2, z2);
-          bq[4 * e + 1][j] = dq_int4_dword_perm(v.y, s2, z2);
-          bq[4 * e + 2][j] = dq_int4_dword_perm(v.z, s2, z2);
-          bq[4 * e + 3][j] = dq_int4_dword_perm(v.w, s2, z2);
+          bq[t][j] = dq_int4_dword_perm(st.w[j][t], s2, z2);
         } else {
-          h2 q[8];
-          dq_int8_dword(v.x, s2, z2, q[0], q[1]);
-          dq_int8_dword(v.y, s2, z2, q[2], q[3]);
-          dq_int8_dword(v.z, s2, z2, q[4], q[5]);
-          dq_int8_dword(v.w, s2, z2, q[6], q[7]);
-          h8 b0, b1;
-          b0.s01 = q[0]; b0.s23 = q[1]; b0.s45 = q[2]; b0.s67 = q[3];
-          b1.s01 = q[4]; b1.s23 = q[5]; b1.s45 = q[6]; b1.s67 = q[7];
-          bq[2 * e + 0][j] = b0;
-          bq[2 * e + 1][j] = b1;
+          h2 q[4];
+          dq_int8_dword(st.w[j][2 * t], s2, z2, q[0], q[1]);
+          dq_int8_dword(st.w[j][2 * t + 1], s2, z2, q[2], q[3]);
+          h8 b;
+          b.s01 = q[0]; b.s23 = q[1]; b.s45 = q[2]; b.s67 = q[3];
+          bq[t][j] = b;
         }
       }
     }
@@ -254,15 +260,16 @@ __global__ __launch_bounds__(64 * NW * KS) void gemmr_kernel(GemmRArgs p) {
   for (int i = 0; i < MB; ++i)
 #pragma unroll
     for (int j = 0; j < NBB; ++j) mfma_result_fence16(acc[i][j]);
-  if constexpr (KS == 2) {
-    // the second k-half's partial sums join the first's through LDS (the
-    // activation buffers are free now): block i of B block j goes to buffer
-    // i & 1 at 16 KiB * (i >> 1), one B block per round
+  {
+    // the other k-parts' partial sums join part 0's through LDS (the
+    // activation buffers are free now), one part and one B block per round:
+    // block i goes to buffer i & 1 at 16 KiB * (i >> 1)
     static_assert(BM * LDSW * 2 >= (MB + 1) / 2 * NW * 16 * 64 * 4, "reduction does not fit");
 #pragma unroll
-    for (int j = 0; j < NBB; ++j) {
+    for (int rj = 0; rj < (KS - 1) * NBB; ++rj) {
+      const int part = 1 + rj / NBB, j = rj % NBB;
       __syncthreads();
-      if (ks == 1) {
+      if (ks == part) {
 #pragma unroll
         for (int i = 0; i < MB; ++i) {
           float* r = (float*)(i & 1 ? lds_a1 : lds_a0) + ((i >> 1) * NW + wc) * 16 * 64 + lane;
@@ -280,7 +287,7 @@ __global__ __launch_bounds__(64 * NW * KS) void gemmr_kernel(GemmRArgs p) {
         }
       }
     }
-    if (ks == 1) return;
+    if (ks != 0) return;
   }
   // lane holds D[row = 8*(v/4) + 4*(lane/32) + v%4][col = lane%32] of each block
   const int rbase = m0 + 4 * h;
@@ -312,11 +319,11 @@ __global__ __launch_bounds__(64 * NW * KS) void gemmr_kernel(GemmRArgs p) {
 
 template <int FMT, int EPI>
 hipError_t launch2(const GemmRArgs& k, int bm, int nwg, hipStream_t s) {
-  constexpr int NW = 4;
+  constexpr int NW = 4, KS = 2;
   if (bm == 128)
-    hipLaunchKernelGGL((gemmr_kernel<FMT, EPI, 128, NW, 2, 2>), dim3(nwg), dim3(128 * NW), 0, s, k);
+    hipLaunchKernelGGL((gemmr_kernel<FMT, EPI, 128, NW, 2, KS>), dim3(nwg), dim3(64 * KS * NW), 0, s, k);
   else
-    hipLaunchKernelGGL((gemmr_kernel<FMT, EPI, 64, NW, 2, 2>), dim3(nwg), dim3(128 * NW), 0, s, k);
+    hipLaunchKernelGGL((gemmr_kernel<FMT, EPI, 64, NW, 2, KS>), dim3(nwg), dim3(64 * KS * NW), 0, s, k);
   return hipGetLastError();
 }
 
