@@ -134,27 +134,32 @@ __global__ __launch_bounds__(64 * NW * KS) void gemmr_kernel(GemmRArgs p) {
     uint16_t s[NBB], z[NBB];
   };
   const int KT = p.K / BK;
+  // The K-tile offset is uniform: it goes in the loads' scalar offset, so a
+  // load costs no per-lane VALU.  Per-lane offsets are kOob for rows past M or
+  // N (those loads read zeros whatever the scalar offset); tiles past K (the
+  // ring's last PF loads, never used) re-read the last tile.
   auto load = [&](int kt, Stage& st) {
-    const bool ok = kt < KT;
+    const int kc = kt < KT ? kt : KT - 1;
+    const uint32_t sa = (uint32_t)(kc * BK * 2);
 #pragma unroll
-    for (int e = 0; e < APT; ++e) st.a[e] = bload16(ar, ok && aoff[e] != kOob ? aoff[e] + kt * BK * 2 : kOob);
-    const uint32_t g2 = (uint32_t)((kt * BK) >> p.gshift) * 2;
+    for (int e = 0; e < APT; ++e)
+      st.a[e] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(ar, aoff[e], sa, 0));
+    const uint32_t sw = (uint32_t)(kc * WROW);
+    const uint32_t g2 = (uint32_t)((kc * BK) >> p.gshift) * 2;
 #pragma unroll
     for (int j = 0; j < NBB; ++j) {
-      const bool wok = ok && woff[j] != kOob;
-      const uint32_t wo = woff[j] + kt * WROW;
 #pragma unroll
       for (int e = 0; e < WL; ++e) {
-        const u4 v = bload16_nt(wr, wok ? wo + 32 * e : kOob);
+        const u4 v = __builtin_bit_cast(
+            u4, __builtin_amdgcn_raw_buffer_load_b128(wr, woff[j] == kOob ? kOob : woff[j] + 32 * e, sw, 2));
         st.w[j][4 * e] = v.x; st.w[j][4 * e + 1] = v.y; st.w[j][4 * e + 2] = v.z; st.w[j][4 * e + 3] = v.w;
       }
       if constexpr (WL == 0) {
-        const uint64_t v = bload8_nt(wr, wok ? wo : kOob);
+        const uint64_t v = __builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(wr, woff[j], sw, 2));
         st.w[j][0] = (uint32_t)v; st.w[j][1] = (uint32_t)(v >> 32);
       }
-      const uint32_t so = wok ? soff[j] + g2 : kOob;
-      st.s[j] = bload2h(sr, so);
-      st.z[j] = bload2h(zr, so);
+      st.s[j] = __builtin_bit_cast(uint16_t, __builtin_amdgcn_raw_buffer_load_b16(sr, soff[j], g2, 0));
+      st.z[j] = __builtin_bit_cast(uint16_t, __builtin_amdgcn_raw_buffer_load_b16(zr, soff[j], g2, 0));
     }
   };
   auto store_a = [&](auto bufc, const Stage& st) {
