@@ -175,6 +175,11 @@ __global__ __launch_bounds__(64 * NW * KS) void gemmr_kernel(GemmRArgs p) {
   };
   // dequantized B fragments of one K-tile: [k-step][block]
   h8 bq0[KKW][NBB], bq1[KKW][NBB];
+  // nibble masks in VGPRs and the fp16 1024 pair in an SGPR: one v_and_or_b32
+  // per nibble pair instead of an AND and an OR with literal operands
+  uint32_t mlo = 0x000F000Fu, mhi = 0x00F000F0u;
+  asm volatile("" : "+v"(mlo), "+v"(mhi));
+  const uint32_t magic = 0x64006400u;
   auto dequant = [&](auto bufc, const Stage& st) {
     constexpr int buf = decltype(bufc)::value;
     auto& bq = buf ? bq1 : bq0;
@@ -185,7 +190,7 @@ __global__ __launch_bounds__(64 * NW * KS) void gemmr_kernel(GemmRArgs p) {
 #pragma unroll
       for (int t = 0; t < KKW; ++t) {
         if (FMT == FMT_INT4) {
-          bq[t][j] = dq_int4_dword_perm(st.w[j][t], s2, z2);
+          bq[t][j] = dq_int4_dword_perm_r(st.w[j][t], s2, z2, mlo, mhi, magic);
         } else {
           h2 q[4];
           dq_int8_dword(st.w[j][2 * t], s2, z2, q[0], q[1]);
