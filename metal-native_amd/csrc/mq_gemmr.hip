@@ -5,10 +5,10 @@
 // (shaders/matmul_dequant_kernel.metal:55-223, :351-479; dispatched at
 // src/ops/matmul.mm:1011-1021).  Same contract as the LDS-staged kernel in
 // mq_gemm.hip: C = A . deq(W)^T, fp16 products accumulated in fp32, one
-// rounding to fp16, optional bias / SwiGLU epilogue.
+// rounding to fp16, optional bias epilogue (SwiGLU stays on the LDS-staged
+// kernel, which measured faster for it).
 //
-//  * A wave owns 32 weight rows (SwiGLU: 32 gate rows and the 32 matching up
-//    rows) across all BM output rows of the workgroup, so every weight is
+//  * A wave owns 32 weight rows across all BM output rows of the workgroup, so every weight is
 //    loaded and dequantized exactly once per workgroup, by the lane that feeds
 //    it to the MFMA: weights never pass through LDS.
 //  * Only the activation tile (BM x 128 k) is shared through LDS, double
@@ -68,7 +68,8 @@ template <int FMT, int EPI, int BM, int NW, int PF, int KS>
 __global__ __launch_bounds__(64 * NW * KS) void gemmr_kernel(GemmRArgs p) {
   constexpr int NT = 64 * NW * KS;
   constexpr int MB = BM / 32;                          // A blocks per wave
-  constexpr int NBB = EPI == EPI_SWIGLU ? 2 : 1;       // B blocks per wave
+  constexpr int NBB = 1;                               // B blocks (32 weight rows) per wave
+  static_assert(EPI != EPI_SWIGLU, "SwiGLU runs on the LDS-staged kernel");
   constexpr int APT = BM * BK / 8 / NT;                // 16-byte activation pieces per thread per K-tile
   constexpr int KKW = 8 / KS;                          // k-steps per wave per K-tile
   constexpr int NDW = FMT == FMT_INT4 ? KKW : 2 * KKW; // weight dwords per lane per B block per K-tile
@@ -111,15 +112,8 @@ __global__ __launch_bounds__(64 * NW * KS) void gemmr_kernel(GemmRArgs p) {
   uint32_t woff[NBB], soff[NBB];
 #pragma unroll
   for (int j = 0; j < NBB; ++j) {
-    bool ok;
-    int grow;
-    if (EPI == EPI_SWIGLU) {
-      ok = col < p.F;
-      grow = j ? p.F + col : col;
-    } else {
-      ok = col < p.N;
-      grow = col;
-    }
+    const bool ok = col < p.N;
+    const int grow = col + j * 32;
     // first byte of this lane's k-steps ks*KKW .. : int4 k-step kk sits at
     // (kk/4)*32 + h*16 + (kk%4)*4, int8 at (kk/2)*32 + h*16 + (kk%2)*8
     const int kk0 = ks * KKW;
@@ -301,21 +295,7 @@ __global__ __launch_bounds__(64 * NW * KS) void gemmr_kernel(GemmRArgs p) {
   }
   // lane holds D[row = 8*(v/4) + 4*(lane/32) + v%4][col = lane%32] of each block
   const int rbase = m0 + 4 * h;
-  if (EPI == EPI_SWIGLU) {
-    if (col < p.F) {
-#pragma unroll
-      for (int i = 0; i < MB; ++i)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int row = rbase + 32 * i + 8 * (v >> 2) + (v & 3);
-          if (row < p.M) {
-            const float gv = (float)(_Float16)acc[i][0][v];
-            const float uv = (float)(_Float16)acc[i][NBB - 1][v];
-            p.C[(int64_t)row * p.ldc + col] = (_Float16)(silu_f32(gv) * uv);
-          }
-        }
-    }
-  } else if (col < p.N) {
+  if (col < p.N) {
     const float bv = (EPI == EPI_BIAS) ? (float)p.bias[col] : 0.f;
 #pragma unroll
     for (int i = 0; i < MB; ++i)
@@ -340,7 +320,7 @@ hipError_t launch2(const GemmRArgs& k, int bm, int nwg, hipStream_t s) {
 template <int FMT>
 hipError_t launch1(const GemmRArgs& k, int epi, int bm, int nwg, hipStream_t s) {
   if (epi == EPI_NONE) return launch2<FMT, EPI_NONE>(k, bm, nwg, s);
-  return launch2<FMT, EPI_BIAS>(k, bm, nwg, s);
+  return launch2<FMT, EPI_BIAS>(k, bm, nwg, s);  // SwiGLU never reaches here
 }
 
 int gshift_of(const LinearArgs& a) {
@@ -359,9 +339,9 @@ bool gemmr_supported(const LinearArgs& a) {
   if (a.G != 1 && (gshift_of(a) < 0 || a.g < BK)) return false;
   if (((uintptr_t)a.A & 15) || (a.lda & 7)) return false;
   if (((uintptr_t)a.W & 15) || (a.ldw & 15)) return false;
-  // SwiGLU (two B blocks per wave) is built into the kernel but not
-  // instantiated: at the Qwen2.5-7B gate+up shape (int8, M = 64) it measured
-  // 89 us against 83 us for the LDS-staged kernel, which keeps that epilogue.
+  // SwiGLU stays on the LDS-staged kernel: a variant of this one with gate
+  // and up blocks in one wave measured 89 us against 83 us there at the
+  // Qwen2.5-7B gate+up shape (int8, M = 64).
   if (a.epi == EPI_SWIGLU) return false;
   const int64_t lim = (int64_t)1 << 31;
   if (((int64_t)(a.M - 1) * a.lda + a.K) * 2 >= lim) return false;
@@ -381,8 +361,7 @@ hipError_t gemmr_launch(const LinearArgs& a, hipStream_t s) {
   const int bm = a.M <= 64 ? 64 : 128;
   const int nw = 4;
   k.nbm = (a.M + bm - 1) / bm;
-  const int cols = a.epi == EPI_SWIGLU ? a.F : a.N;
-  k.nbn = (cols + 32 * nw - 1) / (32 * nw);
+  k.nbn = (a.N + 32 * nw - 1) / (32 * nw);
   const int nwg = k.nbm * k.nbn;
   k.xcd_remap = (nwg % 8 == 0) ? 1 : 0;
   k.a_bytes = (uint32_t)(((int64_t)(a.M - 1) * a.lda + a.K) * 2);
