@@ -264,45 +264,42 @@ __global__ __launch_bounds__(64 * NW * KS) void gemmr_kernel(GemmRArgs p) {
   for (int i = 0; i < MB; ++i)
 #pragma unroll
     for (int j = 0; j < NBB; ++j) mfma_result_fence16(acc[i][j]);
-  {
-    // the other k-parts' partial sums join part 0's through LDS (the
-    // activation buffers are free now), one part and one B block per round:
-    // block i goes to buffer i & 1 at 16 KiB * (i >> 1)
-    static_assert(BM * LDSW * 2 >= (MB + 1) / 2 * NW * 16 * 64 * 4, "reduction does not fit");
+  // The two k-halves' partial sums meet through LDS (the activation buffers
+  // are free now).  Wave ks finishes blocks i with i / (MB/2) == ks: it
+  // receives the other wave's partials of those blocks and hands over its own
+  // of the rest, so both waves share the reduction and the stores.  Block i
+  // of column slice wc sits in buffer i & 1 at 16 KiB * (i >> 1).
+  static_assert(KS == 2 && NBB == 1 && MB % 2 == 0, "the epilogue pairs two k-halves");
+  static_assert(BM * LDSW * 2 >= (MB / 2) * NW * 16 * 64 * 4, "reduction does not fit");
+  auto mine = [&](int i) { return i / (MB / 2) == ks; };
+  __syncthreads();
 #pragma unroll
-    for (int rj = 0; rj < (KS - 1) * NBB; ++rj) {
-      const int part = 1 + rj / NBB, j = rj % NBB;
-      __syncthreads();
-      if (ks == part) {
+  for (int i = 0; i < MB; ++i)
+    if (!mine(i)) {
+      float* r = (float*)(i & 1 ? lds_a1 : lds_a0) + ((i >> 1) * NW + wc) * 16 * 64 + lane;
 #pragma unroll
-        for (int i = 0; i < MB; ++i) {
-          float* r = (float*)(i & 1 ? lds_a1 : lds_a0) + ((i >> 1) * NW + wc) * 16 * 64 + lane;
-#pragma unroll
-          for (int v = 0; v < 16; ++v) r[v * 64] = acc[i][j][v];
-        }
-      }
-      __syncthreads();
-      if (ks == 0) {
-#pragma unroll
-        for (int i = 0; i < MB; ++i) {
-          const float* r = (const float*)(i & 1 ? lds_a1 : lds_a0) + ((i >> 1) * NW + wc) * 16 * 64 + lane;
-#pragma unroll
-          for (int v = 0; v < 16; ++v) acc[i][j][v] += r[v * 64];
-        }
-      }
+      for (int v = 0; v < 16; ++v) r[v * 64] = acc[i][0][v];
     }
-    if (ks != 0) return;
-  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < MB; ++i)
+    if (mine(i)) {
+      const float* r = (const float*)(i & 1 ? lds_a1 : lds_a0) + ((i >> 1) * NW + wc) * 16 * 64 + lane;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][0][v] += r[v * 64];
+    }
   // lane holds D[row = 8*(v/4) + 4*(lane/32) + v%4][col = lane%32] of each block
   const int rbase = m0 + 4 * h;
   if (col < p.N) {
     const float bv = (EPI == EPI_BIAS) ? (float)p.bias[col] : 0.f;
 #pragma unroll
     for (int i = 0; i < MB; ++i)
+      if (mine(i)) {
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int row = rbase + 32 * i + 8 * (v >> 2) + (v & 3);
-        if (row < p.M) p.C[(int64_t)row * p.ldc + col] = (_Float16)(acc[i][0][v] + bv);
+        for (int v = 0; v < 16; ++v) {
+          const int row = rbase + 32 * i + 8 * (v >> 2) + (v & 3);
+          if (row < p.M) p.C[(int64_t)row * p.ldc + col] = (_Float16)(acc[i][0][v] + bv);
+        }
       }
   }
 }
