@@ -26,7 +26,8 @@
 //    two partial sums are added once, through LDS, after the K loop.  With one
 //    wave per slice (and one wave per SIMD) the same kernel took 47 us at the
 //    Llama-3.2-3B QKV shape (M = 512) against 35 us with two; a four-way
-//    split (KS = 4, four waves per SIMD, 8-byte int4 loads) took 44 us.
+//    split (four waves per SIMD, 8-byte int4 loads) took 44 us and was
+//    removed.
 //  * Global loads run PF K-tiles ahead in a register ring; the next tile's
 //    weights are dequantized while this tile's MFMAs run.
 //  * Workgroups sharing a weight slice (same N block, all M blocks) are placed
@@ -73,8 +74,8 @@ __global__ __launch_bounds__(64 * NW * KS) void gemmr_kernel(GemmRArgs p) {
   constexpr int APT = BM * BK / 8 / NT;                // 16-byte activation pieces per thread per K-tile
   constexpr int KKW = 8 / KS;                          // k-steps per wave per K-tile
   constexpr int NDW = FMT == FMT_INT4 ? KKW : 2 * KKW; // weight dwords per lane per B block per K-tile
-  constexpr int WL = NDW / 4;                          // 16-byte weight loads per lane (0: one 8-byte load)
-  static_assert(KS == 2 || KS == 4, "k split");
+  constexpr int WL = NDW / 4;                          // 16-byte weight loads per lane
+  static_assert(KS == 2 && WL >= 1, "two k-halves, whole 16-byte weight loads");
   constexpr int WROW = FMT == FMT_INT4 ? BK / 2 : BK;  // weight bytes per row per K-tile
   static_assert(APT >= 1, "tile too small");
   __shared__ __align__(16) _Float16 lds_a0[BM * LDSW];
@@ -147,10 +148,6 @@ __global__ __launch_bounds__(64 * NW * KS) void gemmr_kernel(GemmRArgs p) {
         const u4 v = __builtin_bit_cast(
             u4, __builtin_amdgcn_raw_buffer_load_b128(wr, woff[j] == kOob ? kOob : woff[j] + 32 * e, sw, 2));
         st.w[j][4 * e] = v.x; st.w[j][4 * e + 1] = v.y; st.w[j][4 * e + 2] = v.z; st.w[j][4 * e + 3] = v.w;
-      }
-      if constexpr (WL == 0) {
-        const uint64_t v = __builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(wr, woff[j], sw, 2));
-        st.w[j][0] = (uint32_t)v; st.w[j][1] = (uint32_t)(v >> 32);
       }
       st.s[j] = __builtin_bit_cast(uint16_t, __builtin_amdgcn_raw_buffer_load_b16(sr, soff[j], g2, 0));
       st.z[j] = __builtin_bit_cast(uint16_t, __builtin_amdgcn_raw_buffer_load_b16(zr, soff[j], g2, 0));
