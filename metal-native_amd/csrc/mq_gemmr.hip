@@ -5,10 +5,11 @@
 // (shaders/matmul_dequant_kernel.metal:55-223, :351-479; dispatched at
 // src/ops/matmul.mm:1011-1021).  Same contract as the LDS-staged kernel in
 // mq_gemm.hip: C = A . deq(W)^T, fp16 products accumulated in fp32, one
-// rounding to fp16, optional bias epilogue (SwiGLU stays on the LDS-staged
-// kernel, which measured faster for it).
+// rounding to fp16, optional bias or SwiGLU epilogue.
 //
-//  * A wave owns 32 weight rows across all BM output rows of the workgroup, so every weight is
+//  * A wave owns 32 weight rows (SwiGLU: half the waves own gate rows, the
+//    other half the matching up rows; the epilogue pairs them through LDS)
+//    across all BM output rows of the workgroup, so every weight is
 //    loaded and dequantized exactly once per workgroup, by the lane that feeds
 //    it to the MFMA: weights never pass through LDS.
 //  * Only the activation tile (BM x 128 k) is shared through LDS, double
@@ -70,7 +71,6 @@ __global__ __launch_bounds__(64 * NW * KS) void gemmr_kernel(GemmRArgs p) {
   constexpr int NT = 64 * NW * KS;
   constexpr int MB = BM / 32;                          // A blocks per wave
   constexpr int NBB = 1;                               // B blocks (32 weight rows) per wave
-  static_assert(EPI != EPI_SWIGLU, "SwiGLU runs on the LDS-staged kernel");
   constexpr int APT = BM * BK / 8 / NT;                // 16-byte activation pieces per thread per K-tile
   constexpr int KKW = 8 / KS;                          // k-steps per wave per K-tile
   constexpr int NDW = FMT == FMT_INT4 ? KKW : 2 * KKW; // weight dwords per lane per B block per K-tile
@@ -109,12 +109,16 @@ __global__ __launch_bounds__(64 * NW * KS) void gemmr_kernel(GemmRArgs p) {
     aoff[e] = row < p.M ? (uint32_t)((row * p.lda + (q % PPR) * 8) * 2) : kOob;
   }
   // weights: B block j of this wave, column fr
-  const int col = nb * 32 * NW + wc * 32 + fr;  // output column
+  // output column; SwiGLU: waves wc < NW/2 own gate rows, wave wc + NW/2 the
+  // matching up rows, and the workgroup covers 16*NW outputs
+  constexpr int NH = NW / 2;
+  const int col = EPI == EPI_SWIGLU ? nb * 32 * NH + (wc % NH) * 32 + fr : nb * 32 * NW + wc * 32 + fr;
+  const bool is_up = EPI == EPI_SWIGLU && wc >= NH;
   uint32_t woff[NBB], soff[NBB];
 #pragma unroll
   for (int j = 0; j < NBB; ++j) {
-    const bool ok = col < p.N;
-    const int grow = col + j * 32;
+    const bool ok = col < (EPI == EPI_SWIGLU ? p.F : p.N);
+    const int grow = (is_up ? p.F + col : col) + j * 32;
     // first byte of this lane's k-steps ks*KKW .. : int4 k-step kk sits at
     // (kk/4)*32 + h*16 + (kk%4)*4, int8 at (kk/2)*32 + h*16 + (kk%2)*8
     const int kk0 = ks * KKW;
@@ -290,7 +294,37 @@ __global__ __launch_bounds__(64 * NW * KS) void gemmr_kernel(GemmRArgs p) {
     }
   // lane holds D[row = 8*(v/4) + 4*(lane/32) + v%4][col = lane%32] of each block
   const int rbase = m0 + 4 * h;
-  if (col < p.N) {
+  if constexpr (EPI == EPI_SWIGLU) {
+    // up waves hand their finished blocks to the matching gate waves (same
+    // LDS slots as the k-half exchange, which every wave has read by now)
+    __syncthreads();
+    if (is_up) {
+#pragma unroll
+      for (int i = 0; i < MB; ++i)
+        if (mine(i)) {
+          float* r = (float*)(i & 1 ? lds_a1 : lds_a0) + ((i >> 1) * NW + wc - NH) * 16 * 64 + lane;
+#pragma unroll
+          for (int v = 0; v < 16; ++v) r[v * 64] = acc[i][0][v];
+        }
+    }
+    __syncthreads();
+    if (!is_up && col < p.F) {
+#pragma unroll
+      for (int i = 0; i < MB; ++i)
+        if (mine(i)) {
+          const float* r = (const float*)(i & 1 ? lds_a1 : lds_a0) + ((i >> 1) * NW + wc) * 16 * 64 + lane;
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const int row = rbase + 32 * i + 8 * (v >> 2) + (v & 3);
+            if (row < p.M) {
+              const float gv = (float)(_Float16)acc[i][0][v];
+              const float uv = (float)(_Float16)r[v * 64];
+              p.C[(int64_t)row * p.ldc + col] = (_Float16)(silu_f32(gv) * uv);
+            }
+          }
+        }
+    }
+  } else if (col < p.N) {
     const float bv = (EPI == EPI_BIAS) ? (float)p.bias[col] : 0.f;
 #pragma unroll
     for (int i = 0; i < MB; ++i)
@@ -317,7 +351,8 @@ hipError_t launch2(const GemmRArgs& k, int bm, int nwg, hipStream_t s) {
 template <int FMT>
 hipError_t launch1(const GemmRArgs& k, int epi, int bm, int nwg, hipStream_t s) {
   if (epi == EPI_NONE) return launch2<FMT, EPI_NONE>(k, bm, nwg, s);
-  return launch2<FMT, EPI_BIAS>(k, bm, nwg, s);  // SwiGLU never reaches here
+  if (epi == EPI_BIAS) return launch2<FMT, EPI_BIAS>(k, bm, nwg, s);
+  return launch2<FMT, EPI_SWIGLU>(k, bm, nwg, s);
 }
 
 int gshift_of(const LinearArgs& a) {
@@ -336,10 +371,7 @@ bool gemmr_supported(const LinearArgs& a) {
   if (a.G != 1 && (gshift_of(a) < 0 || a.g < BK)) return false;
   if (((uintptr_t)a.A & 15) || (a.lda & 7)) return false;
   if (((uintptr_t)a.W & 15) || (a.ldw & 15)) return false;
-  // SwiGLU stays on the LDS-staged kernel: a variant of this one with gate
-  // and up blocks in one wave measured 89 us against 83 us there at the
-  // Qwen2.5-7B gate+up shape (int8, M = 64).
-  if (a.epi == EPI_SWIGLU) return false;
+  if (a.epi == EPI_SWIGLU && a.F * 2 != a.N) return false;
   const int64_t lim = (int64_t)1 << 31;
   if (((int64_t)(a.M - 1) * a.lda + a.K) * 2 >= lim) return false;
   if ((int64_t)a.N * a.ldw >= lim || (int64_t)a.N * a.G * 2 >= lim) return false;
@@ -358,7 +390,7 @@ hipError_t gemmr_launch(const LinearArgs& a, hipStream_t s) {
   const int bm = a.M <= 64 ? 64 : 128;
   const int nw = 4;
   k.nbm = (a.M + bm - 1) / bm;
-  k.nbn = (a.N + 32 * nw - 1) / (32 * nw);
+  k.nbn = a.epi == EPI_SWIGLU ? (a.F + 16 * nw - 1) / (16 * nw) : (a.N + 32 * nw - 1) / (32 * nw);
   const int nwg = k.nbm * k.nbn;
   k.xcd_remap = (nwg % 8 == 0) ? 1 : 0;
   k.a_bytes = (uint32_t)(((int64_t)(a.M - 1) * a.lda + a.K) * 2);
