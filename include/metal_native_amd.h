@@ -46,28 +46,46 @@ enum mq_status {
 /* include/metal_native/ops/matmul.h:60-63 (QuantType) */
 enum mq_quant_type { MQ_QUANT_INT4 = 0, MQ_QUANT_INT8 = 1 };
 
-/* Epilogue applied to the fp32 accumulator before the fp16 store.
- * BIAS: half(acc + float(bias[n]))  (shaders/matmul_fused_epilogue.metal:108-110)
- * SWIGLU: weight rows [0,N/2) are gate, [N/2,N) up; output [M, N/2] =
- *   half(silu(float(half(gate))) * float(half(up))), i.e. the reference's
- *   dequant_matmul followed by fast::swiglu (shaders/fused_swiglu.metal:48-84)
- *   in one kernel. */
-enum mq_epilogue { MQ_EPILOGUE_NONE = 0, MQ_EPILOGUE_BIAS = 1, MQ_EPILOGUE_SWIGLU = 2 };
+/* Epilogue applied to the fp32 accumulator before the one fp16 store, numbered
+ * like the reference's MatmulEpilogue (include/metal_native/ops/fused_matmul.h:18-24,
+ * shaders/matmul_fused_epilogue.metal:97-124):
+ *   BIAS       half(acc + float(bias[n]))
+ *   BIAS_RELU  half(max(acc + float(bias[n]), 0))
+ *   BIAS_SILU  half(v / (1 + exp(-v))), v = acc + float(bias[n])
+ *   RESIDUAL   half(acc + float(residual[m * ldr + n]))
+ * plus SWIGLU (no MatmulEpilogue counterpart): weight rows [0,N/2) are gate,
+ *   [N/2,N) up; output [M, N/2] = half(silu(float(half(gate))) *
+ *   float(half(up))), i.e. the reference's dequant_matmul followed by
+ *   fast::swiglu (shaders/fused_swiglu.metal:48-84) in one kernel. */
+enum mq_epilogue {
+  MQ_EPILOGUE_NONE = 0,
+  MQ_EPILOGUE_BIAS = 1,
+  MQ_EPILOGUE_BIAS_RELU = 2,
+  MQ_EPILOGUE_BIAS_SILU = 3,
+  MQ_EPILOGUE_RESIDUAL = 4,
+  MQ_EPILOGUE_SWIGLU = 5
+};
 
 /* Fused dequantize + matmul: out = epi(A . deq(W)^T).
  * Replaces metal_native::dequant_matmul (include/metal_native/ops/matmul.h:77-82,
  * src/ops/matmul.mm:903-1029; bound as _C.dequant_matmul at
- * bindings/bind_ops.cpp:366-382).  Strides are in elements for A/out and in
- * bytes for the weights (ldw_bytes; K/2 for packed int4 rows, K for int8).
- * zeros may be NULL (no zero term); bias is read only for MQ_EPILOGUE_BIAS.
- * The decode GEMV (M <= 16) splits K across workgroups; its partial sums and
- * counters live in a library workspace kept per (device, stream), allocated
- * by the first call on that stream that needs it (so that call must not be
- * inside stream capture).  Calls on one stream are ordered and share it. */
+ * bindings/bind_ops.cpp:366-382), with the fused epilogues of
+ * metal_native::fused_matmul (src/ops/fused_matmul.mm:132-199).  Strides are
+ * in elements for A/out/residual and in bytes for the weights (ldw_bytes;
+ * K/2 for packed int4 rows, K for int8).  zeros may be NULL (no zero term);
+ * bias is read only by the bias epilogues, residual (fp16 [M, N], row stride
+ * ldr >= N) only by MQ_EPILOGUE_RESIDUAL; the residual may be the output
+ * itself when ldr == ldc (each element is read and then written by one
+ * thread).  The decode GEMV (M <= 16) splits K across workgroups; its
+ * partial sums and counters live in a library workspace kept per (device,
+ * stream), allocated by the first call on that stream that needs it (so that
+ * call must not be inside stream capture).  Calls on one stream are ordered
+ * and share it. */
 MQ_API int mq_dequant_matmul(const void* activations, int64_t lda, const void* weights_packed,
                              int64_t ldw_bytes, const void* scales, const void* zeros, void* out,
                              int64_t ldc, int64_t M, int64_t N, int64_t K, int32_t group_size,
-                             int32_t quant_type, int32_t epilogue, const void* bias, void* stream);
+                             int32_t quant_type, int32_t epilogue, const void* bias, const void* residual,
+                             int64_t ldr, void* stream);
 
 /* Dequantize to fp16 out[N, K] (row stride ldo elements).
  * flat_groups == 0: per-row groups scales[n, k/g], optional zeros (NULL = no
@@ -147,17 +165,19 @@ MQ_API int mq_attention_decode_f16(const void* q, const void* k_cache, const voi
                                    float scale, void* workspace, int64_t workspace_bytes, void* stream);
 
 /* rope_kv + attention_decode in one launch (head_dim 64 or 128, max_len <=
- * 4096): rotates q and the new k from qkv (layout as rope_kv), writes the new
- * k and v into the caches at pos and returns attention_decode's output (one
+ * 4096; mq_attention_decode_rope_supported says whether a shape is taken):
+ * rotates q and the new k from qkv (layout as rope_kv), writes the new k and
+ * v into the caches at pos and returns attention_decode's output (one
  * workgroup per query head; its waves' partial softmax sums are combined in
- * LDS).  The workspace of mq_attention_decode_rope_workspace_size(heads,
- * head_dim, max_len) bytes (-1: shape not supported) is reserved: the current
- * kernel does not read or write it. */
-MQ_API int64_t mq_attention_decode_rope_workspace_size(int32_t heads, int32_t head_dim, int64_t max_len);
+ * LDS).  A device position outside [0, max_len) writes no cache row and
+ * attends over the cache rows that exist: no access outside the caches or
+ * the tables (the host must keep positions in range for a meaningful
+ * result). */
+MQ_API int mq_attention_decode_rope_supported(int32_t heads, int32_t head_dim, int64_t max_len);
 MQ_API int mq_attention_decode_rope_f16(const void* qkv, const float* cos_table, const float* sin_table,
                                         const int64_t* pos, void* k_cache, void* v_cache, void* out, int32_t heads,
                                         int32_t kv_heads, int32_t head_dim, int64_t max_len, float scale,
-                                        void* workspace, int64_t workspace_bytes, void* stream);
+                                        void* stream);
 
 /* Greedy decode tail in one launch (decoder glue, no reference counterpart;
  * replaces torch.argmax + the embedding lookup + the position update of a
@@ -173,21 +193,21 @@ MQ_API int mq_argmax_embed_f16(const void* logits, int64_t vocab, const void* em
                                void* stream);
 
 /* Kernel-path override and layout knobs for tests and tuning (no reference
- * counterpart).  Keys: "force_path" (0 automatic, 2 tiled MFMA GEMM,
- * 3 generic, 6 decode GEMV), "gemv_steps" (K steps per wavefront of the
- * decode GEMV, 1..8, 0 automatic), "gemv_tiles_per_wg" (row tiles per
- * workgroup: 1, 2 or 4, 0 automatic), "gemm_prefetch" (K-tiles the prefill GEMM loads
- * ahead: 2, 4 or 8), "gemm_waves" (wavefronts per 128-row GEMM tile: 4 or 8),
- * "gemm_impl" (prefill GEMM kernel: 0 the register-operand kernel where it applies,
- * 1 always the LDS-staged kernel; both compute the same contract),
- * force_path 7 selects the row-block decode GEMV.  A layout the decode GEMV cannot stage
- * makes it unavailable (the call then takes the tiled or generic kernel).
- * Returns MQ_INVALID_ARGUMENT for an unknown key or value. */
+ * counterpart).  Keys: "force_path" (0 automatic, 2 the prefill GEMM family,
+ * 3 generic, 6 split-K decode GEMV, 7 row-block decode GEMV), "gemv_steps"
+ * (K steps per wavefront of the split-K GEMV, 1..8, 0 automatic),
+ * "gemv_tiles_per_wg" (row tiles per workgroup: 1, 2 or 4, 0 automatic),
+ * "gemm_impl" (prefill GEMM kernel: 0 the register-operand 32x32x16 kernel
+ * where it takes the shape, 1 always the 16x16x32 tiled kernel; both compute
+ * the same contract).  A forced path that cannot take the shape falls back
+ * to the automatic choice.  Returns MQ_INVALID_ARGUMENT for an unknown key or
+ * value. */
 MQ_API int mq_set_option(const char* key, int64_t value);
 
 /* Kernel the last successful mq_dequant_matmul / mq_vecmat_f16 call on this
- * thread launched: 2 tiled GEMM, 3 generic, 4 vecmat [K,N], 6 split-K decode
- * GEMV, 7 row-block decode GEMV. */
+ * thread launched: 2 16x16x32 tiled GEMM, 3 generic, 4 vecmat [K,N], 6
+ * split-K decode GEMV, 7 row-block decode GEMV, 8 register-operand 32x32x16
+ * GEMM. */
 MQ_API int mq_last_path(void);
 
 MQ_API const char* mq_last_error(void);

@@ -9,6 +9,7 @@
 #include <cstring>
 #include <map>
 #include <mutex>
+#include <set>
 #include <string>
 #include <utility>
 
@@ -48,7 +49,16 @@ int num_cus_current() {
 
 // Path ids (mq_last_path / force_path); 1 and 5 are retired ids of earlier
 // decode kernels and are not reused.
-enum Path { PATH_AUTO = 0, PATH_TILED = 2, PATH_GENERIC = 3, PATH_VECMAT_KN = 4, PATH_DECODE = 6, PATH_ROWS = 7 };
+// PATH_TILED selects the prefill GEMM family (force_path); the kernel that ran
+// is reported as PATH_GEMMW (register-operand 32x32x16 GEMM) or PATH_TILED
+// (the 16x16x32 fallback).
+enum Path {
+  PATH_AUTO = 0, PATH_TILED = 2, PATH_GENERIC = 3, PATH_VECMAT_KN = 4, PATH_DECODE = 6, PATH_ROWS = 7,
+  PATH_GEMMW = 8
+};
+// prefill GEMM choice (gemm_impl): 0 the register-operand 32x32x16 kernel
+// where it takes the shape, 1 always the 16x16x32 tiled kernel
+std::atomic<int> g_gemm_impl{0};
 
 mq::GemvTuning gemv_tuning() {
   mq::GemvTuning t;
@@ -105,20 +115,24 @@ hipError_t workspace_for(hipStream_t s, size_t need, void** out) {
 
 bool rows_ok(const mq::LinearArgs& a) { return mq::rows_plan(a, num_cus_current()).ok; }
 
+bool prefill_ok(const mq::LinearArgs& a) {
+  return mq::gemmw_supported(a, num_cus_current()) || mq::tiled_supported(a);
+}
+
 int choose_path(const mq::LinearArgs& a) {
   int forced = g_force_path.load();
   if (forced == PATH_ROWS && rows_ok(a)) return PATH_ROWS;
   if (forced == PATH_DECODE && decode_ok(a)) return PATH_DECODE;
-  if (forced == PATH_TILED && (mq::gemmr_supported(a) || mq::gemm_supported(a) || mq::tiled_supported(a))) return PATH_TILED;
+  if (forced == PATH_TILED && prefill_ok(a)) return PATH_TILED;
   if (forced == PATH_GENERIC) return PATH_GENERIC;
   if (rows_ok(a)) return PATH_ROWS;
   if (decode_ok(a)) return PATH_DECODE;
-  if (mq::gemmr_supported(a) || mq::gemm_supported(a) || mq::tiled_supported(a)) return PATH_TILED;
+  if (prefill_ok(a)) return PATH_TILED;
   return PATH_GENERIC;
 }
 
 int run_linear(const mq::LinearArgs& a, hipStream_t s) {
-  const int path = choose_path(a);
+  int path = choose_path(a);
   hipError_t e;
   if (path == PATH_ROWS) {
     e = mq::rows_launch(a, mq::rows_plan(a, num_cus_current()), s);
@@ -132,10 +146,19 @@ int run_linear(const mq::LinearArgs& a, hipStream_t s) {
     if (e != hipSuccess) return hip_fail(e, "dequant_matmul: workspace allocation failed");
     e = mq::gemv_launch(a, pl, ws, s);
   } else if (path == PATH_TILED) {
-    if (mq::g_gemm_impl == 0 && mq::gemmr_supported(a))
-      e = mq::gemmr_launch(a, s);
-    else
-      e = mq::gemm_supported(a) ? mq::gemm_launch(a, s) : mq::tiled_launch(a, s);
+    const int impl = g_gemm_impl.load();
+    if (impl == 0 && mq::gemmw_supported(a, num_cus_current())) {
+      e = mq::gemmw_launch(a, num_cus_current(), s);
+      path = PATH_GEMMW;
+    } else if (mq::tiled_supported(a)) {
+      e = mq::tiled_launch(a, s);
+    } else if (mq::gemmw_supported(a, num_cus_current())) {
+      e = mq::gemmw_launch(a, num_cus_current(), s);
+      path = PATH_GEMMW;
+    } else {
+      e = mq::generic_linear_launch(a, s);
+      path = PATH_GENERIC;
+    }
   } else {
     e = mq::generic_linear_launch(a, s);
   }
@@ -159,6 +182,10 @@ int build_args(mq::LinearArgs& a, int64_t M, int64_t N, int64_t K, int32_t group
     return fail(MQ_INVALID_ARGUMENT, "dequant_matmul: INT4 weights must be [N, K/2] with K even");
   if (epilogue < MQ_EPILOGUE_NONE || epilogue > MQ_EPILOGUE_SWIGLU)
     return fail(MQ_INVALID_ARGUMENT, "dequant_matmul: unknown epilogue");
+  static_assert(MQ_EPILOGUE_BIAS == mq::EPI_BIAS && MQ_EPILOGUE_BIAS_RELU == mq::EPI_BIAS_RELU &&
+                    MQ_EPILOGUE_BIAS_SILU == mq::EPI_BIAS_SILU && MQ_EPILOGUE_RESIDUAL == mq::EPI_RESIDUAL &&
+                    MQ_EPILOGUE_SWIGLU == mq::EPI_SWIGLU,
+                "C ABI and kernel epilogue numbering agree");
   if (epilogue == MQ_EPILOGUE_SWIGLU && (N & 1))
     return fail(MQ_INVALID_ARGUMENT, "dequant_matmul: SwiGLU needs an even number of weight rows");
   a.M = (int)M;
@@ -174,19 +201,43 @@ int build_args(mq::LinearArgs& a, int64_t M, int64_t N, int64_t K, int32_t group
 
 }  // namespace
 
+namespace mq {
+
+hipError_t allow_dynamic_lds(const void* kernel, int bytes) {
+  static std::mutex mu;
+  static std::set<std::pair<const void*, int>> done;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  std::lock_guard<std::mutex> lk(mu);
+  if (done.count({kernel, dev})) return hipSuccess;
+  e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (e == hipSuccess) done.insert({kernel, dev});
+  return e;
+}
+
+}  // namespace mq
+
 extern "C" {
 
 MQ_API int mq_dequant_matmul(const void* activations, int64_t lda, const void* weights_packed,
                              int64_t ldw_bytes, const void* scales, const void* zeros, void* out,
                              int64_t ldc, int64_t M, int64_t N, int64_t K, int32_t group_size,
-                             int32_t quant_type, int32_t epilogue, const void* bias, void* stream) {
+                             int32_t quant_type, int32_t epilogue, const void* bias, const void* residual,
+                             int64_t ldr, void* stream) {
   mq::LinearArgs a{};
   int rc = build_args(a, M, N, K, group_size, quant_type, epilogue);
   if (rc != MQ_SUCCESS) return rc;
   if (!activations || !weights_packed || !scales || !out)
     return fail(MQ_INVALID_ARGUMENT, "dequant_matmul: null pointer argument");
-  if (epilogue == MQ_EPILOGUE_BIAS && !bias)
+  if (mq::epi_needs_bias(epilogue) && !bias)
     return fail(MQ_INVALID_ARGUMENT, "dequant_matmul: bias epilogue needs a bias pointer");
+  if (epilogue == MQ_EPILOGUE_RESIDUAL) {
+    if (!residual) return fail(MQ_INVALID_ARGUMENT, "dequant_matmul: residual epilogue needs a residual pointer");
+    if (ldr < N) return fail(MQ_INVALID_ARGUMENT, "dequant_matmul: ldr must be >= N");
+    if (residual == out && ldr != ldc)
+      return fail(MQ_INVALID_ARGUMENT, "dequant_matmul: a residual that is the output needs ldr == ldc");
+  }
   const int64_t row_bytes = quant_type == MQ_QUANT_INT4 ? K / 2 : K;
   if (lda < K) return fail(MQ_INVALID_ARGUMENT, "dequant_matmul: lda must be >= K");
   if (ldw_bytes < row_bytes)
@@ -198,6 +249,7 @@ MQ_API int mq_dequant_matmul(const void* activations, int64_t lda, const void* w
   a.A = activations; a.lda = lda;
   a.W = weights_packed; a.ldw = ldw_bytes;
   a.scales = scales; a.zeros = zeros; a.bias = bias;
+  a.resid = residual; a.ldr = ldr;
   a.C = out; a.ldc = ldc;
   return run_linear(a, (hipStream_t)stream);
 }
@@ -220,8 +272,10 @@ MQ_API int mq_rmsnorm_dequant_matmul(const void* x, const void* delta, const voi
   a.C = C; a.ldc = a.epi == mq::EPI_SWIGLU ? a.F : N;
   a.prenorm = 1; a.pre_delta = delta; a.pre_weight = norm_weight; a.pre_resid = resid_out; a.pre_eps = eps;
   if (!weights_packed || !scales || !C) return fail(MQ_INVALID_ARGUMENT, "rmsnorm_dequant_matmul: null pointer argument");
-  if (epilogue == MQ_EPILOGUE_BIAS && !bias)
+  if (mq::epi_needs_bias(epilogue) && !bias)
     return fail(MQ_INVALID_ARGUMENT, "rmsnorm_dequant_matmul: bias epilogue needs a bias pointer");
+  if (epilogue == MQ_EPILOGUE_RESIDUAL)
+    return fail(MQ_INVALID_ARGUMENT, "rmsnorm_dequant_matmul: the residual epilogue is not fused here");
   if (ldw_bytes < (quant_type == MQ_QUANT_INT4 ? K / 2 : K))
     return fail(MQ_INVALID_ARGUMENT, "rmsnorm_dequant_matmul: weight rows too short");
   const mq::RowsPlan pl = mq::rows_plan(a, num_cus_current());
@@ -380,24 +434,21 @@ MQ_API int mq_attention_decode_f16(const void* q, const void* k_cache, const voi
   return MQ_SUCCESS;
 }
 
-MQ_API int64_t mq_attention_decode_rope_workspace_size(int32_t heads, int32_t head_dim, int64_t max_len) {
-  if (heads < 1 || max_len < 1 || !mq::attn_fused_supported(heads, head_dim, max_len)) return -1;
-  return (int64_t)mq::attn_fused_workspace(heads, head_dim, max_len);
+MQ_API int mq_attention_decode_rope_supported(int32_t heads, int32_t head_dim, int64_t max_len) {
+  return heads >= 1 && max_len >= 1 && mq::attn_fused_supported(heads, head_dim, max_len) ? 1 : 0;
 }
 
 MQ_API int mq_attention_decode_rope_f16(const void* qkv, const float* cos_table, const float* sin_table,
                                         const int64_t* pos, void* k_cache, void* v_cache, void* out, int32_t heads,
                                         int32_t kv_heads, int32_t head_dim, int64_t max_len, float scale,
-                                        void* workspace, int64_t workspace_bytes, void* stream) {
-  if (!qkv || !cos_table || !sin_table || !pos || !k_cache || !v_cache || !out || !workspace)
+                                        void* stream) {
+  if (!qkv || !cos_table || !sin_table || !pos || !k_cache || !v_cache || !out)
     return fail(MQ_INVALID_ARGUMENT, "attention_decode_rope: null pointer argument");
   if (heads < 1 || kv_heads < 1 || heads % kv_heads || max_len < 1 ||
       !mq::attn_fused_supported(heads, head_dim, max_len))
     return fail(MQ_INVALID_ARGUMENT, "attention_decode_rope: bad shape (head_dim 64 or 128, max_len <= 4096)");
-  if (workspace_bytes < (int64_t)mq::attn_fused_workspace(heads, head_dim, max_len))
-    return fail(MQ_INVALID_ARGUMENT, "attention_decode_rope: workspace too small");
   hipError_t e = mq::attn_fused_launch(qkv, cos_table, sin_table, pos, k_cache, v_cache, out, heads, kv_heads,
-                                       head_dim, max_len, scale, workspace, (hipStream_t)stream);
+                                       head_dim, max_len, scale, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "attention_decode_rope: kernel launch failed");
   return MQ_SUCCESS;
 }
@@ -431,20 +482,9 @@ MQ_API int mq_set_option(const char* key, int64_t value) {
     g_force_path.store((int)value);
     return MQ_SUCCESS;
   }
-  if (std::strcmp(key, "gemm_prefetch") == 0) {
-    if (value != 2 && value != 4 && value != 8)
-      return fail(MQ_INVALID_ARGUMENT, "set_option: gemm_prefetch must be 2, 4 or 8");
-    mq::g_gemm_pf = (int)value;
-    return MQ_SUCCESS;
-  }
   if (std::strcmp(key, "gemm_impl") == 0) {
     if (value != 0 && value != 1) return fail(MQ_INVALID_ARGUMENT, "set_option: gemm_impl must be 0 or 1");
-    mq::g_gemm_impl = (int)value;
-    return MQ_SUCCESS;
-  }
-  if (std::strcmp(key, "gemm_waves") == 0) {
-    if (value != 4 && value != 8) return fail(MQ_INVALID_ARGUMENT, "set_option: gemm_waves must be 4 or 8");
-    mq::g_gemm_waves = (int)value;
+    g_gemm_impl.store((int)value);
     return MQ_SUCCESS;
   }
   if (std::strcmp(key, "gemv_steps") == 0) {
@@ -480,6 +520,6 @@ MQ_API const char* mq_error_to_string(int code) {
   }
 }
 
-MQ_API int mq_abi_version(void) { return 2; }
+MQ_API int mq_abi_version(void) { return 3; }
 
 }  // extern "C"

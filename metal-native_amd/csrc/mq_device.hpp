@@ -105,6 +105,19 @@ __device__ __forceinline__ h2 nib_byte_pair(uint32_t d, uint32_t sel) {
   return __builtin_elementwise_fma(v, (h2){(_Float16)1.0f, (_Float16)0.0625f},
                                    (h2){(_Float16)-1032.0f, (_Float16)-72.0f});
 }
+// Natural-order variant with the nibble mask in a VGPR and the 0x6400 pair
+// in an SGPR: one v_and_or_b32 per pair instead of an AND and an OR with
+// literal operands (five VALU ops per pair of weights).
+__device__ __forceinline__ h8 dq_int4_dword_nat_r(uint32_t d, h2 s, h2 z, uint32_t mask_v, uint32_t magic_s) {
+  const h2 m = (h2){(_Float16)1.0f, (_Float16)0.0625f};
+  const h2 o = (h2){(_Float16)-1032.0f, (_Float16)-72.0f};
+  h8 r;
+  r.s01 = scale_sub(__builtin_elementwise_fma(as_h2(and_or(__builtin_amdgcn_perm(0u, d, 0x0c000c00u), mask_v, magic_s)), m, o), s, z);
+  r.s23 = scale_sub(__builtin_elementwise_fma(as_h2(and_or(__builtin_amdgcn_perm(0u, d, 0x0c010c01u), mask_v, magic_s)), m, o), s, z);
+  r.s45 = scale_sub(__builtin_elementwise_fma(as_h2(and_or(__builtin_amdgcn_perm(0u, d, 0x0c020c02u), mask_v, magic_s)), m, o), s, z);
+  r.s67 = scale_sub(__builtin_elementwise_fma(as_h2(and_or(__builtin_amdgcn_perm(0u, d, 0x0c030c03u), mask_v, magic_s)), m, o), s, z);
+  return r;
+}
 __device__ __forceinline__ h8 dq_int4_dword_nat(uint32_t d, h2 s, h2 z) {
   h8 r;
   r.s01 = scale_sub(nib_byte_pair(d, 0x0c000c00u), s, z);
@@ -192,6 +205,20 @@ __device__ __forceinline__ void mfma_result_fence16(f16v& v) {
 }
 
 __device__ __forceinline__ float silu_f32(float v) { return v / (1.0f + expf(-v)); }
+
+// Element-wise epilogue on the fp32 accumulator of output (row, col), before
+// the one fp16 rounding (shaders/matmul_fused_epilogue.metal:97-124): bias
+// add, bias + ReLU, bias + SiLU v/(1+exp(-v)), residual add.  The switch is
+// on a kernel argument (uniform), outside the K loop.
+__device__ __forceinline__ float epi_apply(float v, int64_t row, int col, const EpiArgs& e) {
+  switch (e.epi) {
+    case EPI_BIAS: return v + (float)((const _Float16*)e.bias)[col];
+    case EPI_BIAS_RELU: return fmaxf(v + (float)((const _Float16*)e.bias)[col], 0.0f);
+    case EPI_BIAS_SILU: return silu_f32(v + (float)((const _Float16*)e.bias)[col]);
+    case EPI_RESIDUAL: return v + (float)((const _Float16*)e.resid)[row * e.ldr + col];
+    default: return v;
+  }
+}
 
 // Scalar dequant of one element (generic kernels).
 __device__ __forceinline__ _Float16 dq_scalar(int q, _Float16 s, _Float16 z) {

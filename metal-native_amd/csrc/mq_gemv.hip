@@ -50,7 +50,8 @@ constexpr size_t kCntBytes = 65536;  // split-K counters at the start of the wor
 struct GemvKArgs {
   const _Float16* A; int64_t lda;
   const unsigned char* W; int64_t ldw;
-  const _Float16* scales; const _Float16* zeros; const _Float16* bias;
+  const _Float16* scales; const _Float16* zeros;
+  EpiArgs ep;   // element-wise epilogue (kernels without SwiGLU)
   _Float16* C; int64_t ldc;
   int M, K, N, F, G, gshift;
   int T;        // row tiles
@@ -271,11 +272,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvKArgs p) {
     } else {
       const int row = t * RPW + r;
       if (holder && row < p.N) {
-        const float bv = (EPI == EPI_BIAS) ? (float)p.bias[row] : 0.f;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int i = 4 * gi + e;
-          if (i < M) p.C[(int64_t)i * p.ldc + row] = (_Float16)(v[e] + bv);
+          if (i < M) p.C[(int64_t)i * p.ldc + row] = (_Float16)epi_apply(v[e], i, row, p.ep);
         }
       }
     }
@@ -333,8 +333,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvKArgs p) {
       const float* src = p.part + (int64_t)i * NP + row;
       float s = 0.f;
       for (int sp = 0; sp < p.P; ++sp) s += ld_coherent(src + sp * pstride);
-      if (EPI == EPI_BIAS) s += (float)p.bias[row];
-      p.C[(int64_t)i * p.ldc + row] = (_Float16)s;
+      p.C[(int64_t)i * p.ldc + row] = (_Float16)epi_apply(s, i, row, p.ep);
     }
   }
   if (tid == 0) __hip_atomic_store(p.cnt + q, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
@@ -342,12 +341,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvKArgs p) {
 
 template <int FMT, int EPI, int RPW, int KK>
 hipError_t launch4(const GemvKArgs& k, const GemvPlan& pl, hipStream_t s) {
-  static bool attr = false;
   auto fn = gemv_kernel<FMT, EPI, RPW, KK>;
-  if (!attr && pl.lds_bytes > 65536) {
-    hipError_t e = hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, 163840);
+  if (pl.lds_bytes > 65536) {
+    hipError_t e = allow_dynamic_lds((const void*)fn, 163840);
     if (e != hipSuccess) return e;
-    attr = true;
   }
   hipLaunchKernelGGL(fn, dim3(pl.nwg), dim3(64 * pl.tpw), pl.lds_bytes, s, k);
   return hipGetLastError();
@@ -375,8 +372,7 @@ hipError_t launch2(const GemvKArgs& k, const GemvPlan& pl, hipStream_t s) {
 
 template <int FMT>
 hipError_t launch1(const GemvKArgs& k, const GemvPlan& pl, int epi, hipStream_t s) {
-  if (FMT == FMT_F16 || epi == EPI_NONE) return launch2<FMT, EPI_NONE>(k, pl, s);
-  if (epi == EPI_BIAS) return launch2<FMT, EPI_BIAS>(k, pl, s);
+  if (FMT == FMT_F16 || epi != EPI_SWIGLU) return launch2<FMT, EPI_NONE>(k, pl, s);
   return launch2<FMT, EPI_SWIGLU>(k, pl, s);
 }
 
@@ -481,7 +477,7 @@ hipError_t gemv_launch(const LinearArgs& a, const GemvPlan& pl, void* ws, hipStr
   k.A = (const _Float16*)a.A; k.lda = a.lda;
   k.W = (const unsigned char*)a.W; k.ldw = a.ldw;
   k.scales = (const _Float16*)a.scales; k.zeros = (const _Float16*)a.zeros;
-  k.bias = (const _Float16*)a.bias;
+  k.ep = a.epi_args();
   k.C = (_Float16*)a.C; k.ldc = a.ldc;
   k.M = a.M; k.K = a.K; k.N = a.N; k.F = a.F; k.G = a.G;
   k.gshift = gshift_of(a);

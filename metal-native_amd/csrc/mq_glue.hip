@@ -10,11 +10,6 @@
 
 #include <algorithm>
 
-// Timing probe points; empty unless a benchmark harness defines MQ_GTRACE.
-#ifndef MQ_GTRACE
-#define MQ_GTRACE(slot)
-#endif
-
 namespace mq {
 namespace {
 
@@ -102,9 +97,13 @@ __global__ __launch_bounds__(1024) void add_rmsnorm_kernel(_Float16* x, const _F
 __global__ __launch_bounds__(256) void rope_kv_kernel(const _Float16* qkv, const float* cos_t, const float* sin_t,
                                                        const int64_t* pos_p, _Float16* q_out, _Float16* kc,
                                                        _Float16* vc, int H, int KVH, int D, int64_t L) {
+  // a position outside [0, L) writes no cache row and reads the nearest
+  // table row: never an access outside the caches or the tables
   const int64_t pos = *pos_p;
-  const float* cs = cos_t + pos * D;
-  const float* sn = sin_t + pos * D;
+  const bool in = pos >= 0 && pos < L;
+  const int64_t pt = pos < 0 ? 0 : (pos < L ? pos : L - 1);
+  const float* cs = cos_t + pt * D;
+  const float* sn = sin_t + pt * D;
   const int half = D / 2;
   const int total = (H + 2 * KVH) * D;
   for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < total; e += gridDim.x * blockDim.x) {
@@ -115,11 +114,17 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(const _Float16* qkv, const
       const float rot = j < half ? -pair : pair;
       const _Float16 y = (_Float16)(x * cs[j] + rot * sn[j]);
       if (head < H) q_out[e] = y;
-      else kc[((int64_t)(head - H) * L + pos) * D + j] = y;
-    } else {
+      else if (in) kc[((int64_t)(head - H) * L + pos) * D + j] = y;
+    } else if (in) {
       vc[((int64_t)(head - H - KVH) * L + pos) * D + j] = (_Float16)x;
     }
   }
+}
+
+// Cache positions attended to for the device position pos: 0..pos, clamped
+// to the cache (a position at or past L reads no row past the cache).
+__device__ __forceinline__ int positions_in_cache(int64_t pos, int64_t L) {
+  return (int)(pos < 0 ? 1 : (pos < L ? pos + 1 : L));
 }
 
 // Single-token attention, split over positions (flash-decoding): workgroup
@@ -136,7 +141,7 @@ __global__ __launch_bounds__(64) void attn_partial_kernel(const _Float16* q, con
   __shared__ float ps[kSplit];
   const int c = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
   const int kvh = h / (H / KVH);
-  const int n = (int)(*pos_p) + 1;
+  const int n = positions_in_cache(*pos_p, L);
   const int t0 = c * kSplit;
   float* rec = ws + ((int64_t)h * gridDim.x + c) * (D + 2);  // [m, l, o[D]]
   if (t0 >= n) {  // split past the last position: empty record
@@ -194,7 +199,7 @@ __global__ __launch_bounds__(64) void attn_partial_d_kernel(const _Float16* q, c
   __shared__ float pv[kSplit * (D + 1)];
   const int c = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
   const int kvh = h / (H / KVH);
-  const int n = (int)(*pos_p) + 1;
+  const int n = positions_in_cache(*pos_p, L);
   const int t0 = c * kSplit;
   float* rec = ws + ((int64_t)h * gridDim.x + c) * (D + 2);  // [m, l, o[D]]
   if (t0 >= n) {
@@ -321,11 +326,14 @@ __global__ __launch_bounds__(768) void attn_head_d_kernel(const _Float16* qkv, c
     }
   };
   load_rows(w);   // NW <= nsplit: every wave has a first split
-  MQ_GTRACE(0);
+  // positions outside [0, L): no cache write, attention over the cache rows
+  // that exist, the nearest table row (no access outside any buffer)
   const int64_t pos = *pos_p;
-  const int n = (int)pos + 1;
-  const float* cs = cos_t + pos * D;
-  const float* sn = sin_t + pos * D;
+  const bool in = pos >= 0 && pos < L;
+  const int n = positions_in_cache(pos, L);
+  const int64_t pt = pos < 0 ? 0 : (pos < L ? pos : L - 1);
+  const float* cs = cos_t + pt * D;
+  const float* sn = sin_t + pt * D;
   auto rope = [&](const _Float16* src, int j) -> _Float16 {
     const float x = (float)src[j];
     const float pair = (float)src[j < HALF ? j + HALF : j - HALF];
@@ -336,20 +344,19 @@ __global__ __launch_bounds__(768) void attn_head_d_kernel(const _Float16* qkv, c
     const _Float16* qrow = qkv + h * D;
     const _Float16* krow = qkv + (H + kvh) * D;
     const _Float16* vsrc = qkv + (H + KVH + kvh) * D;
-    const int64_t prow = ((int64_t)kvh * L + pos) * D;
+    const int64_t prow = ((int64_t)kvh * L + pt) * D;
     for (int j = tid; j < D; j += blockDim.x) {
       qs[j] = (float)rope(qrow, j);
       const _Float16 kn = rope(krow, j), vn = vsrc[j];
       kn16[j] = kn;
       vn16[j] = vn;
-      if (h % grp == 0) {
+      if (in && h % grp == 0) {
         kc[prow + j] = kn;
         vc[prow + j] = vn;
       }
     }
   }
   __syncthreads();
-  MQ_GTRACE(1);
   h2 qh[4];   // q is an fp16 value (rounded as rope_kv stores it)
 #pragma unroll
   for (int e = 0; e < 4; ++e) qh[e] = (h2){(_Float16)qs[8 * q + 2 * e], (_Float16)qs[8 * q + 2 * e + 1]};
@@ -357,7 +364,7 @@ __global__ __launch_bounds__(768) void attn_head_d_kernel(const _Float16* qkv, c
   for (int c = w; c < nsplit; c += NW) {
     const int t0 = c * SUB;
     if (t0 >= n) break;   // this and the wave's later steps lie past the new token
-    if (pos >= t0 && pos < t0 + SUB) {   // the split holding the new token: its row from registers
+    if (in && pos >= t0 && pos < t0 + SUB) {   // the split holding the new token: its row from registers
       const h8 kn = *(const h8*)(kn16 + 8 * q), vn = *(const h8*)(vn16 + 8 * q);
 #pragma unroll
       for (int i = 0; i < NI; ++i)
@@ -414,13 +421,11 @@ __global__ __launch_bounds__(768) void attn_head_d_kernel(const _Float16* qkv, c
     for (int e = 0; e < 8; ++e) o_run[e] = o_run[e] * a + o[e] * bsc;
     m_run = mn;
   }
-  MQ_GTRACE(2);
   if (lane == 0) { wm[w] = m_run; wl[w] = l_run; }
   if (rg == 0)
 #pragma unroll
     for (int e = 0; e < 8; ++e) wo[w][8 * q + e] = o_run[e];
   __syncthreads();
-  MQ_GTRACE(3);
   if (w == 0 && rg == 0) {
     float mm = -INFINITY;
     for (int ww = 0; ww < NW; ++ww) mm = fmaxf(mm, wm[ww]);
@@ -436,7 +441,6 @@ __global__ __launch_bounds__(768) void attn_head_d_kernel(const _Float16* qkv, c
     for (int e = 0; e < 8; ++e) r[e] = (_Float16)(o[e] / ll);
     *(h8*)(out + h * D + 8 * q) = r;
   }
-  MQ_GTRACE(4);
 }
 
 // ---- greedy decode tail: token = argmax(logits), pos += 1, x = embed[token] ----
@@ -568,18 +572,12 @@ hipError_t attn_decode_launch(const void* q, const void* kc, const void* vc, con
   return hipGetLastError();
 }
 
-size_t attn_fused_workspace(int, int, int64_t) {
-  return 256;   // reserved: the one-workgroup-per-head kernel combines its splits in LDS
-}
-
 bool attn_fused_supported(int H, int D, int64_t L) {
   return H >= 1 && (D == 64 || D == 128) && (L + kSplit - 1) / kSplit <= 64;
 }
 
 hipError_t attn_fused_launch(const void* qkv, const float* cos_t, const float* sin_t, const int64_t* pos, void* kc,
-                             void* vc, void* out, int H, int KVH, int D, int64_t L, float scale, void* ws,
-                             hipStream_t s) {
-  (void)ws;
+                             void* vc, void* out, int H, int KVH, int D, int64_t L, float scale, hipStream_t s) {
   const int NW = std::min<int64_t>(12, (L + 4095 / D) / (4096 / D));   // one wave per step up to 12
   if (D == 128)
     hipLaunchKernelGGL(attn_head_d_kernel<128>, dim3(H), dim3(64 * NW), 0, s, (const _Float16*)qkv, cos_t, sin_t,

@@ -8,7 +8,23 @@
 namespace mq {
 
 enum Fmt { FMT_INT4 = 0, FMT_INT8 = 1, FMT_F16 = 2 };
-enum Epi { EPI_NONE = 0, EPI_BIAS = 1, EPI_SWIGLU = 2 };
+// Epilogues, numbered like the reference's MatmulEpilogue
+// (include/metal_native/ops/fused_matmul.h:18-24), plus SwiGLU.  The first
+// five are element-wise on the fp32 accumulator (EpiArgs below); SwiGLU pairs
+// two weight rows per output and changes a kernel's shape, so kernels take it
+// as a template parameter and the element-wise ones as a run-time value.
+enum Epi { EPI_NONE = 0, EPI_BIAS = 1, EPI_BIAS_RELU = 2, EPI_BIAS_SILU = 3, EPI_RESIDUAL = 4, EPI_SWIGLU = 5 };
+__host__ __device__ inline bool epi_needs_bias(int e) { return e == EPI_BIAS || e == EPI_BIAS_RELU || e == EPI_BIAS_SILU; }
+
+// Operands of the element-wise epilogues: bias fp16 [N], residual fp16
+// [M, N] with row stride ldr elements (it may be the output itself when
+// ldr == ldc: every output element is read and written by one thread).
+struct EpiArgs {
+  const void* bias;
+  const void* resid;
+  int64_t ldr;
+  int epi;
+};
 
 // One quantized (or fp16) linear: C[M, Nout] = epi(A[M,K] . W[N,K]^T).
 struct LinearArgs {
@@ -18,13 +34,16 @@ struct LinearArgs {
   int64_t ldw;          // row stride of W in bytes
   const void* scales;   // fp16 [N, G] (unused for fp16 W)
   const void* zeros;    // fp16 [N, G] or nullptr (= no zero term)
-  const void* bias;     // fp16 [N] for EPI_BIAS
+  const void* bias;     // fp16 [N] for the bias epilogues
+  const void* resid;    // fp16 [M, N] (row stride ldr) for EPI_RESIDUAL
+  int64_t ldr;
   void* C;              // fp16 [M, Nout], row stride ldc (elements)
   int64_t ldc;
   int M, N, K;
   int g, G;             // group size along K, groups per row
   int fmt;              // Fmt
   int epi;              // Epi
+  __host__ __device__ EpiArgs epi_args() const { return EpiArgs{bias, resid, ldr, epi}; }
   int F;                // SwiGLU half width (N = 2F), 0 otherwise
   // Optional fused pre-norm (row-block GEMV, M = 1): the activations are
   // A' = half(A + pre_delta) (pre_delta may be null), written to pre_resid by
@@ -35,6 +54,10 @@ struct LinearArgs {
   void* pre_resid = nullptr;
   float pre_eps = 0.f;
 };
+
+// Raise a kernel's dynamic LDS limit to `bytes` on the current device, once
+// per (kernel, device); thread-safe.
+hipError_t allow_dynamic_lds(const void* kernel, int bytes);
 
 // Split-K MFMA GEMV (decode, M <= 16).
 struct GemvTuning {
@@ -65,15 +88,9 @@ struct RowsPlan {
 RowsPlan rows_plan(const LinearArgs& a, int num_cus);
 hipError_t rows_launch(const LinearArgs& a, const RowsPlan& p, hipStream_t s);
 
-// 32x32x16 MFMA GEMM with register-ring prefetch (prefill).
-extern int g_gemm_pf;     // K-tiles in flight ahead of the MFMAs (2, 4 or 8)
-extern int g_gemm_waves;  // wavefronts per workgroup for 128-row tiles (4 or 8)
-bool gemm_supported(const LinearArgs& a);
-// register-B GEMM (weights dequantized into MFMA operands, activations via LDS)
-extern int g_gemm_impl;  // 0: register-B kernel where supported, 1: LDS-staged kernel
-bool gemmr_supported(const LinearArgs& a);
-hipError_t gemmr_launch(const LinearArgs& a, hipStream_t s);
-hipError_t gemm_launch(const LinearArgs& a, hipStream_t s);
+// Register-operand 32x32x16 MFMA GEMM (prefill default).
+bool gemmw_supported(const LinearArgs& a, int num_cus);
+hipError_t gemmw_launch(const LinearArgs& a, int num_cus, hipStream_t s);
 
 // 16x16x32 MFMA GEMM, K steps of 32 (fallback for shapes the GEMM above does not take).
 bool tiled_supported(const LinearArgs& a);
@@ -110,13 +127,10 @@ hipError_t rope_kv_launch(const void* qkv, const float* cos_t, const float* sin_
                           void* kc, void* vc, int H, int KVH, int D, int64_t L, hipStream_t s);
 size_t attn_decode_workspace(int H, int D, int64_t L);
 // rotary + cache write + attention in one launch, one workgroup per query head
-// (head_dim 64 or 128, L <= 4096); ws: attn_fused_workspace bytes, reserved
-// (the kernel does not touch it)
-size_t attn_fused_workspace(int H, int D, int64_t L);
+// (head_dim 64 or 128, L <= 4096)
 bool attn_fused_supported(int H, int D, int64_t L);
 hipError_t attn_fused_launch(const void* qkv, const float* cos_t, const float* sin_t, const int64_t* pos, void* kc,
-                             void* vc, void* out, int H, int KVH, int D, int64_t L, float scale, void* ws,
-                             hipStream_t s);
+                             void* vc, void* out, int H, int KVH, int D, int64_t L, float scale, hipStream_t s);
 hipError_t attn_decode_launch(const void* q, const void* kc, const void* vc, const int64_t* pos, void* out, int H,
                               int KVH, int D, int64_t L, float scale, void* ws, hipStream_t s);
 

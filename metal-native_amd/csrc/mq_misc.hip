@@ -150,10 +150,8 @@ __global__ __launch_bounds__(256) void generic_linear_kernel(LinearArgs p, int n
       float gv = (float)(_Float16)accs[0];
       float uv = (float)(_Float16)accs[1];
       C[(int64_t)m * p.ldc + j] = (_Float16)(silu_f32(gv) * uv);
-    } else if (p.epi == EPI_BIAS) {
-      C[(int64_t)m * p.ldc + j] = (_Float16)(accs[0] + (float)((const _Float16*)p.bias)[j]);
     } else {
-      C[(int64_t)m * p.ldc + j] = (_Float16)accs[0];
+      C[(int64_t)m * p.ldc + j] = (_Float16)epi_apply(accs[0], m, j, p.epi_args());
     }
   }
 }

@@ -37,26 +37,12 @@
 #include <algorithm>
 #include <cmath>
 
-// Timing probe points; empty unless a benchmark harness defines MQ_TRACE.
-#ifndef MQ_TRACE
-#define MQ_TRACE(slot)
-#endif
-
 namespace mq {
 namespace {
 
-#ifndef MQ_ROWS_KD
-#define MQ_ROWS_KD 4
-#endif
-#ifndef MQ_ROWS_KPRE
-#define MQ_ROWS_KPRE 2
-#endif
-constexpr int kD = MQ_ROWS_KD;     // ring depth (units in flight per wave)
-#ifndef MQ_ROWS_NW
-#define MQ_ROWS_NW 12
-#endif
-constexpr int kNW = MQ_ROWS_NW;  // wavefronts per workgroup
-constexpr int kPre = MQ_ROWS_KPRE;  // ring slots issued before the staging data is waited for
+constexpr int kD = 4;        // ring depth (units in flight per wave)
+constexpr int kNW = 12;      // wavefronts per workgroup
+constexpr int kPre = 2;      // ring slots issued before the staging data is waited for
 constexpr int kXB = 8;           // activation pieces per thread per staging batch
 constexpr int kSB = 2;           // scale/zero pieces per thread per staging batch
 constexpr size_t kLds = 163840;  // LDS per CU on gfx950
@@ -64,7 +50,8 @@ constexpr size_t kLds = 163840;  // LDS per CU on gfx950
 struct RowsKArgs {
   const _Float16* A; int64_t lda;
   const unsigned char* W; int64_t ldw;
-  const _Float16* scales; const _Float16* zeros; const _Float16* bias;
+  const _Float16* scales; const _Float16* zeros;
+  EpiArgs ep;     // element-wise epilogue (kernels without SwiGLU)
   _Float16* C; int64_t ldc;
   int M, K, N, F, G, gshift;
   int R;          // output rows (SwiGLU: output columns) per workgroup
@@ -106,7 +93,6 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
   const int nl = lane & 15, gi = lane >> 4;
   const int r = nl % RPW, sh = nl / RPW;              // weight row in tile, K shift
   const int klane = sh * 4 * KPL + gi * KPL;          // this lane's k within a unit
-  MQ_TRACE(0);
 
   // ---- this workgroup's weight rows ----
   // local weight row lr: plain lr = t*RPW + r (global row0 + lr); SwiGLU the
@@ -304,7 +290,6 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
     // every wave's staging loads reach the texture unit first (a plain
     // barrier: it does not wait for the loads) ...
     __builtin_amdgcn_s_barrier();
-    MQ_TRACE(5);
     // ... then a short head of the weight stream.  The staging data is waited
     // for before the rest: a wave blocks while the memory queues are full, so
     // a deep stream issued first would hold back the start of compute.
@@ -314,7 +299,6 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
     for (int e = 0; e < kXB; ++e) asm volatile("" : "+v"(xv[e]));
 #pragma unroll
     for (int e = 0; e < kSB; ++e) asm volatile("" : "+v"(sv[e]), "+v"(zv[e]));
-    MQ_TRACE(6);
     if (PRE) {
       // A' = half(A + delta) (the residual, stored by workgroup 0), then the
       // row's sum of squares across the workgroup, then the normalised pieces
@@ -361,7 +345,6 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
     if (FMT != FMT_F16) s_put(0, sv, zv, nsb);
 #pragma unroll
     for (int d = kPre; d < kD; ++d) raw[d] = wload();
-    MQ_TRACE(7);
   }
   // the rest (large M*K, many scale rows) after the ring
   for (int base = kXB * NT; base < npieces; base += kXB * NT) {
@@ -376,7 +359,6 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
   }
   // LDS barrier that leaves the weight loads in flight
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  MQ_TRACE(1);
 
   // ---- stream ----
   const int xrow = min(r, M - 1) * p.XS;
@@ -471,9 +453,7 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
       raw[d] = wload();
     }
   }
-  MQ_TRACE(2);
   __syncthreads();
-  MQ_TRACE(3);
 
   // ---- sum the slots per output, epilogue ----
   const int MR = M * RPW;
@@ -498,23 +478,16 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
     for (int idx = tid; idx < M * valid; idx += NT) {
       const int i = idx / valid, lr = idx - i * valid;
       const int t = lr / RPW, rr = lr - t * RPW;
-      float v = tile_sum(t, i, rr);
-      if (EPI == EPI_BIAS) v += (float)p.bias[row0 + lr];
-      p.C[(int64_t)i * p.ldc + row0 + lr] = (_Float16)v;
+      p.C[(int64_t)i * p.ldc + row0 + lr] = (_Float16)epi_apply(tile_sum(t, i, rr), i, row0 + lr, p.ep);
     }
   }
-  MQ_TRACE(4);
 }
 
 template <int FMT, int EPI, int RPW, bool PRE>
 hipError_t launch4(const RowsKArgs& k, const RowsPlan& pl, hipStream_t s) {
-  static bool attr = false;
   auto fn = rows_kernel<FMT, EPI, RPW, PRE>;
-  if (!attr) {
-    hipError_t e = hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLds);
-    if (e != hipSuccess) return e;
-    attr = true;
-  }
+  hipError_t e = allow_dynamic_lds((const void*)fn, (int)kLds);
+  if (e != hipSuccess) return e;
   hipLaunchKernelGGL(fn, dim3(pl.nwg), dim3(64 * kNW), pl.lds_bytes, s, k);
   return hipGetLastError();
 }
@@ -539,8 +512,7 @@ hipError_t launch2(const RowsKArgs& k, const RowsPlan& pl, hipStream_t s) {
 
 template <int FMT>
 hipError_t launch1(const RowsKArgs& k, const RowsPlan& pl, int epi, hipStream_t s) {
-  if (FMT == FMT_F16 || epi == EPI_NONE) return launch2<FMT, EPI_NONE>(k, pl, s);
-  if (epi == EPI_BIAS) return launch2<FMT, EPI_BIAS>(k, pl, s);
+  if (FMT == FMT_F16 || epi != EPI_SWIGLU) return launch2<FMT, EPI_NONE>(k, pl, s);
   return launch2<FMT, EPI_SWIGLU>(k, pl, s);
 }
 
@@ -639,7 +611,7 @@ hipError_t rows_launch(const LinearArgs& a, const RowsPlan& pl, hipStream_t s) {
   k.A = (const _Float16*)a.A; k.lda = a.lda;
   k.W = (const unsigned char*)a.W; k.ldw = a.ldw;
   k.scales = (const _Float16*)a.scales; k.zeros = (const _Float16*)a.zeros;
-  k.bias = (const _Float16*)a.bias;
+  k.ep = a.epi_args();
   k.C = (_Float16*)a.C; k.ldc = a.ldc;
   k.M = a.M; k.K = a.K; k.N = a.N; k.F = a.F; k.G = a.G;
   k.gshift = gshift_of(a);

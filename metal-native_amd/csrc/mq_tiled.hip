@@ -26,7 +26,8 @@ constexpr int kThreads = 256;
 struct TiledKArgs {
   const _Float16* A; int64_t lda;
   const unsigned char* W; int64_t ldw;
-  const _Float16* scales; const _Float16* zeros; const _Float16* bias;
+  const _Float16* scales; const _Float16* zeros;
+  EpiArgs ep;
   _Float16* C; int64_t ldc;
   int M, N, K, g, G, F, gshift;
 };
@@ -188,11 +189,10 @@ __global__ __launch_bounds__(kThreads, 2) void tiled_kernel(TiledKArgs p) {
       for (int j = 0; j < 4; ++j) {
         int col = nb * BN + wn * 64 + 16 * j + (lane & 15);
         if (col >= p.N) continue;
-        float bv = (EPI == EPI_BIAS) ? (float)p.bias[col] : 0.f;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           int m = m0 + wm * 64 + 16 * i + 4 * (lane >> 4) + r;
-          if (m < p.M) p.C[(int64_t)m * p.ldc + col] = (_Float16)(acc[i][j][r] + bv);
+          if (m < p.M) p.C[(int64_t)m * p.ldc + col] = (_Float16)epi_apply(acc[i][j][r], m, col, p.ep);
         }
       }
   }
@@ -200,11 +200,10 @@ __global__ __launch_bounds__(kThreads, 2) void tiled_kernel(TiledKArgs p) {
 
 template <int FMT>
 hipError_t launch_fmt(const TiledKArgs& k, int epi, dim3 grid, hipStream_t s) {
-  switch (epi) {
-    case EPI_NONE: hipLaunchKernelGGL((tiled_kernel<FMT, EPI_NONE>), grid, dim3(kThreads), 0, s, k); break;
-    case EPI_BIAS: hipLaunchKernelGGL((tiled_kernel<FMT, EPI_BIAS>), grid, dim3(kThreads), 0, s, k); break;
-    default: hipLaunchKernelGGL((tiled_kernel<FMT, EPI_SWIGLU>), grid, dim3(kThreads), 0, s, k); break;
-  }
+  if (epi == EPI_SWIGLU)
+    hipLaunchKernelGGL((tiled_kernel<FMT, EPI_SWIGLU>), grid, dim3(kThreads), 0, s, k);
+  else
+    hipLaunchKernelGGL((tiled_kernel<FMT, EPI_NONE>), grid, dim3(kThreads), 0, s, k);
   return hipGetLastError();
 }
 
@@ -225,7 +224,7 @@ hipError_t tiled_launch(const LinearArgs& a, hipStream_t s) {
   k.A = (const _Float16*)a.A; k.lda = a.lda;
   k.W = (const unsigned char*)a.W; k.ldw = a.ldw;
   k.scales = (const _Float16*)a.scales; k.zeros = (const _Float16*)a.zeros;
-  k.bias = (const _Float16*)a.bias;
+  k.ep = a.epi_args();
   k.C = (_Float16*)a.C; k.ldc = a.ldc;
   k.M = a.M; k.N = a.N; k.K = a.K; k.g = a.g; k.G = a.G; k.F = a.F;
   k.gshift = -1;

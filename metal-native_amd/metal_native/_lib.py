@@ -23,11 +23,15 @@ INVALID_ARGUMENT = 4
 QUANT_INT4 = 0
 QUANT_INT8 = 1
 
+# include/metal_native/ops/fused_matmul.h:18-24 numbering, plus SwiGLU
 EPILOGUE_NONE = 0
 EPILOGUE_BIAS = 1
-EPILOGUE_SWIGLU = 2
+EPILOGUE_BIAS_RELU = 2
+EPILOGUE_BIAS_SILU = 3
+EPILOGUE_RESIDUAL = 4
+EPILOGUE_SWIGLU = 5
 
-PATH_NAMES = {0: "none", 2: "tiled", 3: "generic", 4: "vecmat_kn", 6: "decode", 7: "rows"}
+PATH_NAMES = {0: "none", 2: "tiled", 3: "generic", 4: "vecmat_kn", 6: "decode", 7: "rows", 8: "gemmw"}
 
 _c_void_p = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -36,7 +40,8 @@ _i32 = ctypes.c_int32
 # name -> (restype, argtypes)
 SIGNATURES = {
     "mq_dequant_matmul": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p,
-                                 _i64, _i64, _i64, _i64, _i32, _i32, _i32, _c_void_p, _c_void_p]),
+                                 _i64, _i64, _i64, _i64, _i32, _i32, _i32, _c_void_p, _c_void_p, _i64,
+                                 _c_void_p]),
     "mq_dequantize": (_i32, [_c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64,
                              _i32, _i32, _i32, _c_void_p]),
     "mq_rmsnorm_dequant_matmul": (_i32, [_c_void_p, _c_void_p, _c_void_p, ctypes.c_float, _c_void_p, _c_void_p,
@@ -53,10 +58,9 @@ SIGNATURES = {
     "mq_rope_kv_f16": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                               _i32, _i32, _i32, _i64, _c_void_p]),
     "mq_attention_decode_workspace_size": (_i64, [_i32, _i32, _i64]),
-    "mq_attention_decode_rope_workspace_size": (_i64, [_i32, _i32, _i64]),
+    "mq_attention_decode_rope_supported": (_i32, [_i32, _i32, _i64]),
     "mq_attention_decode_rope_f16": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
-                                            _c_void_p, _i32, _i32, _i32, _i64, ctypes.c_float, _c_void_p, _i64,
-                                            _c_void_p]),
+                                            _c_void_p, _i32, _i32, _i32, _i64, ctypes.c_float, _c_void_p]),
     "mq_attention_decode_f16": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i32, _i32, _i32,
                                        _i64, ctypes.c_float, _c_void_p, _i64, _c_void_p]),
     "mq_argmax_embed_workspace_size": (_i64, [_i64]),

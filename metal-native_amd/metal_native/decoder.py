@@ -140,8 +140,6 @@ class SyntheticDecoder:
         self.positions = torch.arange(cfg.max_len, device=self.device)
         # two residual-stream buffers (the fused norm + GEMV writes out of place)
         self.resid = torch.zeros((2, 1, d), dtype=torch.float16, device=self.device)
-        # fused rotary + attention workspace (reserved by the current kernel)
-        self.attn_ws = ops.attention_decode_rope_workspace(cfg.heads, cfg.head_dim, cfg.max_len, self.device)
         # greedy decode chain: the next step's embedding row and the tail workspace
         self.x0 = torch.zeros((1, d), dtype=torch.float16, device=self.device)
         self.tail_ws = ops.argmax_embed_workspace(cfg.vocab, self.device)
@@ -167,7 +165,7 @@ class SyntheticDecoder:
             x = bufs[cur]
             cur ^= 1
             a = ops.attention_decode_rope(qkv, self.cos, self.sin, pos, self.kv[li, 0], self.kv[li, 1], H, KVH, Dh,
-                                          scale, self.attn_ws)
+                                          scale)
             act = ops.rmsnorm_dequant_matmul(x, L["o"](a), L["ln2"], cfg.eps, bufs[cur], *L["gate_up"].operands(),
                                              epilogue="swiglu")
             x = bufs[cur]
@@ -228,6 +226,9 @@ class SyntheticDecoder:
 def decode_tokens_per_second(model: SyntheticDecoder, n_tokens: int = 64, warmup: int = 3) -> dict:
     """Greedy-decode ``n_tokens`` tokens after the prefilled cache, each step a
     replay of one captured HIP graph; returns tokens/s and ms/token."""
+    if model.prefilled + n_tokens > model.cfg.max_len:
+        raise ValueError(f"decode_tokens_per_second: {model.prefilled} prefilled + {n_tokens} tokens exceed the "
+                         f"KV cache of {model.cfg.max_len} positions")
     dev = model.device
     tok = torch.zeros(1, dtype=torch.int64, device=dev)
     pos = torch.full((1,), model.prefilled, dtype=torch.int64, device=dev)

@@ -65,13 +65,19 @@ def _require_cuda(t: torch.Tensor, what: str, op: str):
         _invalid(f"{op}: {what} must be a GPU tensor (got {t.device})")
 
 
-def _rows(t: torch.Tensor, what: str, op: str) -> int:
-    """Row stride (elements) of a 2-D tensor whose last dim is contiguous."""
+def _rowmajor(t: torch.Tensor, what: str, op: str) -> tuple[torch.Tensor, int]:
+    """``(t', ld)``: a 2-D tensor whose rows the kernels can address as
+    ``base + i * ld`` with unit stride along the last dimension, and that
+    row stride in elements.  A tensor whose rows overlap or alias (a
+    broadcast ``expand``, an ``as_strided`` view with ``stride(0) < size(1)``)
+    or whose last dimension is strided is copied to a contiguous tensor
+    first, so a kernel never reads past the storage it was given."""
     if t.dim() != 2:
         _invalid(f"{op}: {what} must be 2D")
-    if t.size(1) > 1 and t.stride(1) != 1:
-        _invalid(f"{op}: {what} must be contiguous along its last dimension")
-    return max(t.stride(0), t.size(1)) if t.size(0) > 1 else t.size(1)
+    rows, cols = t.shape
+    if (cols > 1 and t.stride(1) != 1) or (rows > 1 and t.stride(0) < cols):
+        t = t.contiguous()
+    return t, (t.stride(0) if rows > 1 else cols)
 
 
 # ---------------------------------------------------------------------------
@@ -79,7 +85,10 @@ def _rows(t: torch.Tensor, what: str, op: str) -> int:
 # ---------------------------------------------------------------------------
 
 _EPILOGUES = {None: _lib.EPILOGUE_NONE, "none": _lib.EPILOGUE_NONE,
-              "bias": _lib.EPILOGUE_BIAS, "swiglu": _lib.EPILOGUE_SWIGLU}
+              "bias": _lib.EPILOGUE_BIAS, "bias_relu": _lib.EPILOGUE_BIAS_RELU,
+              "bias_silu": _lib.EPILOGUE_BIAS_SILU, "residual": _lib.EPILOGUE_RESIDUAL,
+              "swiglu": _lib.EPILOGUE_SWIGLU}
+_BIAS_EPILOGUES = (_lib.EPILOGUE_BIAS, _lib.EPILOGUE_BIAS_RELU, _lib.EPILOGUE_BIAS_SILU)
 
 
 def quant_type_code(quant_type: str) -> int:
@@ -90,7 +99,8 @@ def quant_type_code(quant_type: str) -> int:
 
 def dequant_matmul(activations: torch.Tensor, weights_packed: torch.Tensor, scales: torch.Tensor,
                    zeros: torch.Tensor, group_size: int, quant_type: str, *,
-                   epilogue: str | None = None, bias: torch.Tensor | None = None) -> torch.Tensor:
+                   epilogue: str | None = None, bias: torch.Tensor | None = None,
+                   residual: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
     """Fused dequantize + matmul: ``activations[M,K] . deq(weights)[N,K]^T`` -> fp16 ``[M,N]``.
 
     Validation and messages follow src/ops/matmul.mm:910-934.  Beyond the
@@ -98,9 +108,15 @@ def dequant_matmul(activations: torch.Tensor, weights_packed: torch.Tensor, scal
     too (the reference reads out of bounds on a mismatch), and
     ``group_size == K`` (one group per row: per-output-channel scales) is
     accepted as an extension.
-    ``epilogue="bias"`` adds ``bias[N]`` in fp32; ``epilogue="swiglu"`` treats
+    Epilogues (fp32, before the one fp16 rounding; the reference's
+    MatmulEpilogue set, include/metal_native/ops/fused_matmul.h:18-24):
+    ``"bias"`` adds ``bias[N]``, ``"bias_relu"`` / ``"bias_silu"`` then apply
+    ReLU / SiLU, ``"residual"`` adds ``residual[M, N]`` (which may be ``out``
+    itself, for an in-place residual add).  ``epilogue="swiglu"`` treats
     weight rows ``[0,N/2)`` as gate and ``[N/2,N)`` as up and returns
-    ``[M, N/2] = fast.swiglu(gate, up)`` of the fp16 projection.
+    ``[M, N/2] = fast.swiglu(gate, up)`` of the fp16 projection.  ``out``
+    (extension): an fp16 ``[M, N_out]`` tensor with unit column stride to
+    write instead of a new one.
     """
     op = "dequant_matmul"
     _require_cuda(activations, "activations", op)
@@ -140,31 +156,54 @@ def dequant_matmul(activations: torch.Tensor, weights_packed: torch.Tensor, scal
     if epilogue not in _EPILOGUES:
         _invalid(f"{op}: unknown epilogue {epilogue!r}")
     epi = _EPILOGUES[epilogue]
-    if epi == _lib.EPILOGUE_BIAS:
+    if epi in _BIAS_EPILOGUES:
         if bias is None:
-            _invalid(f"{op}: epilogue='bias' needs bias")
+            _invalid(f"{op}: epilogue={epilogue!r} needs bias")
         _require_cuda(bias, "bias", op)
         if bias.dtype != torch.float16 or bias.numel() != N:
             _invalid(f"{op}: bias must be Float16 [N]")
         bias = bias.contiguous()
     elif bias is not None:
-        _invalid(f"{op}: bias given without epilogue='bias'")
+        _invalid(f"{op}: bias given without a bias epilogue")
+    if epi == _lib.EPILOGUE_RESIDUAL:
+        if residual is None:
+            _invalid(f"{op}: epilogue='residual' needs residual")
+        _require_cuda(residual, "residual", op)
+        if residual.dtype != torch.float16 or tuple(residual.shape) != (M, N):
+            _invalid(f"{op}: residual must be Float16 [M, N] = [{M}, {N}]")
+    elif residual is not None:
+        _invalid(f"{op}: residual given without epilogue='residual'")
     if epi == _lib.EPILOGUE_SWIGLU and N % 2:
         _invalid(f"{op}: SwiGLU needs an even number of weight rows")
     n_out = N // 2 if epi == _lib.EPILOGUE_SWIGLU else N
 
-    lda = _rows(activations, "activations", op)
-    ldw = _rows(weights_packed, "weights_packed", op)
+    activations, lda = _rowmajor(activations, "activations", op)
+    weights_packed, ldw = _rowmajor(weights_packed, "weights_packed", op)
     scales = scales.contiguous()
     zeros = zeros.contiguous()
     dev = activations.device
-    out = torch.empty((M, n_out), dtype=torch.float16, device=dev)
+    if out is None:
+        out = torch.empty((M, n_out), dtype=torch.float16, device=dev)
+    else:
+        _require_cuda(out, "out", op)
+        if out.dtype != torch.float16 or tuple(out.shape) != (M, n_out) or (n_out > 1 and out.stride(1) != 1) \
+                or (M > 1 and out.stride(0) < n_out):
+            _invalid(f"{op}: out must be Float16 [{M}, {n_out}] with unit column stride")
+    ldc = out.stride(0) if M > 1 else n_out
+    ldr = 0
+    if residual is not None:
+        if residual.data_ptr() == out.data_ptr():
+            if residual.stride() != out.stride():
+                _invalid(f"{op}: a residual that is the output must have the output's strides")
+            ldr = ldc
+        else:
+            residual, ldr = _rowmajor(residual, "residual", op)
     if M == 0 or n_out == 0:
         return out
     with torch.cuda.device(dev):
         rc = _L.mq_dequant_matmul(
             _ptr(activations), lda, _ptr(weights_packed), ldw, _ptr(scales), _ptr(zeros), _ptr(out),
-            n_out, M, N, K, group_size, qt, epi, _ptr(bias), _stream_handle(dev))
+            ldc, M, N, K, group_size, qt, epi, _ptr(bias), _ptr(residual), ldr, _stream_handle(dev))
     _check(rc)
     return out
 
@@ -221,7 +260,7 @@ def dequantize(weights_packed: torch.Tensor, scales: torch.Tensor, zeros: torch.
                 _invalid(f"{op}: zeros must be Float16 [N, ceil(K/group_size)]")
             zeros = zeros.contiguous()
     scales = scales.contiguous()
-    ldw = _rows(weights_packed, "weights_packed", op)
+    weights_packed, ldw = _rowmajor(weights_packed, "weights_packed", op)
     dev = weights_packed.device
     out = torch.empty((N, K), dtype=torch.float16, device=dev)
     if N == 0 or K == 0:
@@ -325,14 +364,15 @@ def matmul(a: torch.Tensor, b: torch.Tensor, transpose_a: bool = False,
         a2 = a2.contiguous()
     if b.stride(-1) != 1:
         b = b.contiguous()
+    b, ldb = _rowmajor(b, "b", op)
     rows = a2.shape[0]
     out = torch.empty((rows, N), dtype=torch.float16, device=a.device)
     dev = a.device
     with torch.cuda.device(dev):
         for r0 in range(0, rows, 64):
             r1 = min(rows, r0 + 64)
-            ai = a2[r0:r1]
-            rc = _L.mq_vecmat_f16(_ptr(ai), _rows(ai, "a", op), _ptr(b), _rows(b, "b", op),
+            ai, lda = _rowmajor(a2[r0:r1], "a", op)
+            rc = _L.mq_vecmat_f16(_ptr(ai), lda, _ptr(b), ldb,
                                   _ptr(out[r0:r1]), N, r1 - r0, N, K, 1 if transpose_b else 0,
                                   _stream_handle(dev))
             _check(rc)
@@ -422,8 +462,9 @@ def rmsnorm_dequant_matmul(x: torch.Tensor, delta: torch.Tensor | None, norm_wei
             and _L.mq_rmsnorm_dequant_matmul_supported(N, K, group_size, qt, epi)):
         n_out = N // 2 if epi == _lib.EPILOGUE_SWIGLU else N
         out = torch.empty((1, n_out), dtype=torch.float16, device=x.device)
+        weights_packed, ldw = _rowmajor(weights_packed, "weights_packed", "dequant_matmul")
         rc = _L.mq_rmsnorm_dequant_matmul(_ptr(x), _ptr(delta), _ptr(norm_weight), float(eps), _ptr(resid_out),
-                                          _ptr(weights_packed), _rows(weights_packed, "weights_packed", "dequant_matmul"),
+                                          _ptr(weights_packed), ldw,
                                           _ptr(scales), _ptr(zeros), _ptr(out), N, K, group_size, qt, epi, _ptr(bias),
                                           _stream_handle(x.device))
         if rc == 0:
@@ -436,28 +477,23 @@ def rmsnorm_dequant_matmul(x: torch.Tensor, delta: torch.Tensor | None, norm_wei
                           bias=bias)
 
 
-def attention_decode_rope_workspace(heads: int, head_dim: int, max_len: int, device) -> torch.Tensor | None:
-    """Zeroed workspace for ``attention_decode_rope`` (None when the fused
-    kernel does not take the shape); keep one per stream."""
-    nb = _L.mq_attention_decode_rope_workspace_size(heads, head_dim, max_len)
-    if nb < 0:
-        return None
-    return torch.zeros(nb, dtype=torch.uint8, device=device)
+def attention_decode_rope_supported(heads: int, head_dim: int, max_len: int) -> bool:
+    """Whether ``attention_decode_rope`` runs the one-launch kernel for this shape."""
+    return bool(_L.mq_attention_decode_rope_supported(heads, head_dim, max_len))
 
 
 def attention_decode_rope(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, pos: torch.Tensor,
                           k_cache: torch.Tensor, v_cache: torch.Tensor, heads: int, kv_heads: int, head_dim: int,
-                          scale: float, workspace: torch.Tensor | None) -> torch.Tensor:
-    """``rope_kv`` followed by ``attention_decode``: one launch with a
-    workspace from ``attention_decode_rope_workspace``, else (None) the two
-    separate kernels."""
-    if workspace is None:
+                          scale: float) -> torch.Tensor:
+    """``rope_kv`` followed by ``attention_decode``: one launch where
+    ``attention_decode_rope_supported``, else the two separate kernels."""
+    if not attention_decode_rope_supported(heads, head_dim, k_cache.shape[1]):
         q = rope_kv(qkv, cos, sin, pos, k_cache, v_cache, heads, kv_heads, head_dim)
         return attention_decode(q, k_cache, v_cache, pos, scale)
     out = torch.empty((1, heads * head_dim), dtype=torch.float16, device=qkv.device)
     _check(_L.mq_attention_decode_rope_f16(_ptr(qkv), _ptr(cos), _ptr(sin), _ptr(pos), _ptr(k_cache), _ptr(v_cache),
                                            _ptr(out), heads, kv_heads, head_dim, k_cache.shape[1], float(scale),
-                                           _ptr(workspace), workspace.numel(), _stream_handle(qkv.device)))
+                                           _stream_handle(qkv.device)))
     return out
 
 

@@ -31,8 +31,10 @@ Semantics restated
 * SwiGLU: ``half(silu(float(g)) * float(u))`` with ``silu(v) = v / (1+exp(-v))``
   applied to the fp16 outputs of the projection
   (shaders/fused_swiglu.metal:48-84; src/future/future_stubs.mm:61-101).
-* bias epilogue: ``half(acc + float(bias[n]))``
-  (shaders/matmul_fused_epilogue.metal:97-124).
+* fused epilogues on the fp32 accumulator, one rounding after
+  (shaders/matmul_fused_epilogue.metal:97-124): bias ``half(acc + float(b[n]))``,
+  bias+ReLU ``half(max(acc + b, 0))``, bias+SiLU ``half(v / (1 + exp(-v)))``,
+  residual ``half(acc + float(r[m, n]))``.
 
 Why fp32-then-round equals fp16 arithmetic: for one +, - or x of two fp16
 values the exact result rounded to fp32 (p=24 >= 2*11+2) and then to fp16 is
@@ -173,11 +175,14 @@ def matmul_f32acc(a: np.ndarray, w: np.ndarray) -> np.ndarray:
     return np.asarray(a, np.float16).astype(np.float32) @ np.asarray(w, np.float16).astype(np.float32).T
 
 
-def apply_epilogue(acc: np.ndarray, epilogue: str | None, bias=None) -> np.ndarray:
+def apply_epilogue(acc: np.ndarray, epilogue: str | None, bias=None, residual=None) -> np.ndarray:
     """Round the fp32 accumulator to fp16 after the optional epilogue.
 
     * ``None``   -> ``half(acc)`` (matmul_dequant_kernel.metal:217)
     * ``"bias"`` -> ``half(acc + float(bias[n]))`` (matmul_fused_epilogue.metal:108-110)
+    * ``"bias_relu"`` -> ``half(max(0, acc + float(bias[n])))`` (:111-113)
+    * ``"bias_silu"`` -> ``half(v / (1 + exp(-v)))``, ``v = acc + float(bias[n])`` (:114-117)
+    * ``"residual"`` -> ``half(acc + float(residual[m, n]))`` (:118-121)
     * ``"swiglu"`` -> columns ``[0,F)`` are gate, ``[F,2F)`` up; the projection
       is rounded to fp16 first and then ``fused_swiglu_fp16`` is applied,
       which is the reference's two-dispatch composition
@@ -185,8 +190,15 @@ def apply_epilogue(acc: np.ndarray, epilogue: str | None, bias=None) -> np.ndarr
     """
     if epilogue is None or epilogue == "none":
         return acc.astype(np.float16)
-    if epilogue == "bias":
-        return (acc + np.asarray(bias, np.float16).astype(np.float32)[None, :]).astype(np.float16)
+    if epilogue in ("bias", "bias_relu", "bias_silu"):
+        v = (acc + np.asarray(bias, np.float16).astype(np.float32)[None, :]).astype(np.float32)
+        if epilogue == "bias_relu":
+            v = np.maximum(v, np.float32(0.0))
+        elif epilogue == "bias_silu":
+            v = silu_f32(v)
+        return v.astype(np.float16)
+    if epilogue == "residual":
+        return (acc + np.asarray(residual, np.float16).astype(np.float32)).astype(np.float16)
     if epilogue == "swiglu":
         F = acc.shape[1] // 2
         h = acc.astype(np.float16)
@@ -195,7 +207,7 @@ def apply_epilogue(acc: np.ndarray, epilogue: str | None, bias=None) -> np.ndarr
 
 
 def dequant_matmul(a, bp, scales, zeros, group_size: int, quant_type: str,
-                   epilogue: str | None = None, bias=None) -> np.ndarray:
+                   epilogue: str | None = None, bias=None, residual=None) -> np.ndarray:
     """``_C.dequant_matmul`` semantics (bindings/bind_ops.cpp:366-382 ->
     src/ops/matmul.mm:903-1029 -> shaders/matmul_dequant_kernel.metal),
     for *every* row of A (the reference's M<=8 kernel writes only row 0; the
@@ -204,7 +216,7 @@ def dequant_matmul(a, bp, scales, zeros, group_size: int, quant_type: str,
     a = np.asarray(a, dtype=np.float16)
     K = a.shape[1]
     w = dequantize(bp, scales, zeros, K, group_size, quant_type)
-    return apply_epilogue(matmul_f32acc(a, w), epilogue, bias)
+    return apply_epilogue(matmul_f32acc(a, w), epilogue, bias, residual)
 
 
 def vecmat_f16(a, b, transpose_b: bool) -> np.ndarray:

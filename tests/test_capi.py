@@ -40,7 +40,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version_and_error_strings(lib):
-    assert lib.mq_abi_version() == 2
+    assert lib.mq_abi_version() == 3
     assert lib.mq_error_to_string(0) == b"Success"
     assert lib.mq_error_to_string(4) == b"InvalidArgument"
     assert lib.mq_error_to_string(8) == b"NotImplemented"
@@ -48,9 +48,9 @@ def test_abi_version_and_error_strings(lib):
 
 def test_validation_without_gpu(lib):
     P = ctypes.c_void_p(256)  # never dereferenced: validation fails first
-    call = lambda M, N, K, g, qt, epi, ldw=None: lib.mq_dequant_matmul(
+    call = lambda M, N, K, g, qt, epi, ldw=None, res=None, ldr=0: lib.mq_dequant_matmul(
         P, K, P, (K // 2 if qt == 0 else K) if ldw is None else ldw, P, P, P, N, M, N, K, g, qt, epi,
-        None, None)
+        None, res, ldr, None)
     assert call(0, 8, 32, 32, 0, 0) == 4
     assert b"positive" in lib.mq_last_error()
     assert call(1, 8, 33, 32, 0, 0) == 4  # odd K for int4
@@ -59,10 +59,19 @@ def test_validation_without_gpu(lib):
     assert b"INT4 weights must be [N, K/2]" in lib.mq_last_error()
     assert call(1, 8, 32, 32, 1, 0, ldw=16) == 4
     assert b"INT8 weights must be [N, K]" in lib.mq_last_error()
-    assert call(1, 7, 32, 32, 0, 2) == 4  # SwiGLU needs even N
+    assert call(1, 7, 32, 32, 0, 5) == 4  # SwiGLU needs even N
     assert call(1, 8, 32, 32, 5, 0) == 4
-    assert call(1, 8, 32, 32, 0, 1) == 4  # bias epilogue without bias
-    assert b"bias" in lib.mq_last_error()
+    for epi in (1, 2, 3):  # bias, bias+ReLU, bias+SiLU without bias
+        assert call(1, 8, 32, 32, 0, epi) == 4
+        assert b"bias" in lib.mq_last_error()
+    assert call(1, 8, 32, 32, 0, 4) == 4  # residual epilogue without residual
+    assert b"residual" in lib.mq_last_error()
+    assert call(1, 8, 32, 32, 0, 4, res=P, ldr=7) == 4  # ldr < N
+    assert b"ldr" in lib.mq_last_error()
+    assert call(2, 8, 32, 32, 0, 4, res=P, ldr=16) == 4  # residual aliasing the output with another stride
+    assert b"ldr == ldc" in lib.mq_last_error()
+    assert call(1, 8, 32, 32, 0, 6) == 4
+    assert b"unknown epilogue" in lib.mq_last_error()
     assert lib.mq_dequantize(P, 16, P, P, P, 32, 4, 32, 32, 0, 1, None) == 4  # flat + zeros
     assert lib.mq_swiglu_f16(None, P, P, 10, None) == 4
     assert lib.mq_vecmat_f16(P, 10, P, 10, P, 10, 1, 300, 300, 1, None) == 4  # lda < K
@@ -112,3 +121,46 @@ def test_quantize_needs_a_gpu_tensor():
 
     with pytest.raises(mn.MetalNativeError, match="GPU tensor"):
         mn.quantize(torch.zeros(4, 64, dtype=torch.float16), 32, "int4")
+
+
+def test_rowmajor_copies_overlapping_rows():
+    """A broadcast or overlapping view (row stride below the row length) is
+    handed to the kernels as a contiguous copy, never with a row stride that
+    would read past its storage; ordinary row-major views keep their stride."""
+    import torch
+
+    from metal_native.ops import _rowmajor
+
+    x = torch.arange(8, dtype=torch.float16).reshape(1, 8)
+    e = x.expand(64, 8)                       # stride (0, 1)
+    t, ld = _rowmajor(e, "activations", "op")
+    assert ld == 8 and t.is_contiguous() and t.shape == (64, 8)
+    assert torch.equal(t, e)
+    base = torch.arange(64, dtype=torch.float16)
+    o = base.as_strided((10, 8), (4, 1))      # rows overlap by half
+    t, ld = _rowmajor(o, "activations", "op")
+    assert ld == 8 and torch.equal(t, o)
+    big = torch.zeros(16, 24, dtype=torch.float16)
+    v = big[:, :8]                            # row stride 24 >= 8: kept
+    t, ld = _rowmajor(v, "activations", "op")
+    assert ld == 24 and t.data_ptr() == v.data_ptr()
+    one = big[3:4, :8]                        # a single row: stride unused
+    t, ld = _rowmajor(one, "activations", "op")
+    assert ld == 8 and t.data_ptr() == one.data_ptr()
+    col = big[:, :8].t()                      # strided last dimension: copied
+    t, ld = _rowmajor(col, "activations", "op")
+    assert t.is_contiguous() and ld == 16
+
+
+def test_decode_loop_refuses_positions_past_the_cache():
+    """The decode benchmark checks on the host that every position it will
+    write lies inside the KV cache."""
+    import types
+
+    import pytest as _pt
+
+    from metal_native.decoder import DecoderConfig, decode_tokens_per_second
+
+    model = types.SimpleNamespace(prefilled=512, cfg=DecoderConfig(max_len=576), device=None)
+    with _pt.raises(ValueError, match="exceed the KV cache"):
+        decode_tokens_per_second(model, n_tokens=65)

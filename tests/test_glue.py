@@ -103,8 +103,7 @@ def test_fused_rope_attention_matches_separate_kernels(gpu, H, KVH, D, L, pos):
     g.manual_seed(pos + D)
     kc0 = torch.randn((KVH, L, D), device=gpu, generator=g).half()
     vc0 = torch.randn((KVH, L, D), device=gpu, generator=g).half()
-    ws = ops.attention_decode_rope_workspace(H, D, L, gpu)
-    assert ws is not None
+    assert ops.attention_decode_rope_supported(H, D, L)
     scale = 1.0 / math.sqrt(D)
     for rep in range(3):
         qkv = torch.randn((1, (H + 2 * KVH) * D), device=gpu, generator=g).half()
@@ -113,7 +112,7 @@ def test_fused_rope_attention_matches_separate_kernels(gpu, H, KVH, D, L, pos):
         q = ops.rope_kv(qkv, cos, sin, p, k1, v1, H, KVH, D)
         want = ops.attention_decode(q, k1, v1, p, scale)
         k2, v2 = kc0.clone(), vc0.clone()
-        got = ops.attention_decode_rope(qkv, cos, sin, p, k2, v2, H, KVH, D, scale, ws)
+        got = ops.attention_decode_rope(qkv, cos, sin, p, k2, v2, H, KVH, D, scale)
         assert torch.equal(k1, k2) and torch.equal(v1, v2)
         err = (got.float() - want.float()).abs()
         assert float(err.max()) <= 1e-3 * (1 + float(want.float().abs().max())), (rep, float(err.max()))
@@ -183,3 +182,35 @@ def test_argmax_embed(gpu, V, case):
         assert int(tok.item()) == want
         assert int(pos.item()) == 42 + rep
         assert torch.equal(x[0], embed[want])
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_positions_past_the_cache_touch_nothing(gpu, D):
+    """A device position at or past the cache end (a caller bug) writes no
+    cache row and reads only rows that exist: the caches are unchanged and
+    the attention output is the finite softmax over the whole cache."""
+    from metal_native import ops
+    from metal_native.decoder import DecoderConfig, rope_tables
+
+    H, KVH, L = 8, 2, 256
+    cfg = DecoderConfig(heads=H, kv_heads=KVH, head_dim=D, max_len=L)
+    cos, sin = rope_tables(cfg, gpu)
+    g = torch.Generator(device=gpu)
+    g.manual_seed(D)
+    kc = torch.randn((KVH, L, D), device=gpu, generator=g).half()
+    vc = torch.randn((KVH, L, D), device=gpu, generator=g).half()
+    qkv = torch.randn((1, (H + 2 * KVH) * D), device=gpu, generator=g).half()
+    scale = 1.0 / math.sqrt(D)
+    for pos in (L, L + 100):
+        p = torch.tensor([pos], device=gpu)
+        k1, v1 = kc.clone(), vc.clone()
+        q = ops.rope_kv(qkv, cos, sin, p, k1, v1, H, KVH, D)
+        out = ops.attention_decode(q, k1, v1, p, scale)
+        k2, v2 = kc.clone(), vc.clone()
+        out2 = ops.attention_decode_rope(qkv, cos, sin, p, k2, v2, H, KVH, D, scale)
+        torch.cuda.synchronize()
+        assert torch.equal(k1, kc) and torch.equal(v1, vc)
+        assert torch.equal(k2, kc) and torch.equal(v2, vc)
+        assert torch.isfinite(out.float()).all() and torch.isfinite(out2.float()).all()
+        want = attention_ref(q, kc, vc, L - 1, scale)
+        assert float((out.float() - want.float()).abs().max()) <= 1e-2

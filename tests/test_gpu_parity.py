@@ -26,6 +26,9 @@ TOL_REL = 1e-3
 GOLD = os.path.join(os.path.dirname(__file__), "golden", "known_answers.npz")
 
 PATHS = {"tiled": 2, "generic": 3, "decode": 6, "rows": 7}
+# force_path "tiled" selects the prefill GEMM family; the kernel that ran is
+# reported as "gemmw" (register-operand GEMM) or "tiled" (16x16x32 fallback)
+FAMILY = {"gemmw": "tiled"}
 
 
 @pytest.fixture(scope="module")
@@ -83,6 +86,26 @@ def check_swiglu(y, acc, what):
                            f"max abs err {err.max():.3g}")
 
 
+def check_epilogue(y, acc, epi, what, bias=None, residual=None):
+    """Element-wise epilogues against the oracle's closed forms in float64
+    (the bar is the matmul tolerance plus, for SiLU, the change of silu(v)
+    across one fp32 rounding of v; exp differs by ulps between libraries)."""
+    v = acc.astype(np.float64)
+    if bias is not None:
+        v = v + bias.astype(np.float64)[None, :]
+    if residual is not None:
+        v = v + residual.astype(np.float64)
+    if epi == "bias_relu":
+        v = np.maximum(v, 0.0)
+    elif epi == "bias_silu":
+        with np.errstate(over="ignore"):
+            v = v / (1.0 + np.exp(-v))
+    y = y.astype(np.float64)
+    err = np.abs(y - v)
+    bad = err > TOL_ABS + TOL_REL * np.abs(v)
+    assert not bad.any(), f"{what}: {bad.sum()} of {bad.size} outside tolerance; max abs err {err.max():.3g}"
+
+
 def run_dm(mn, gpu, x, wp, s, z, g, qt, path=None, **kw):
     mn.set_option("force_path", PATHS[path] if path else 0)
     try:
@@ -91,7 +114,7 @@ def run_dm(mn, gpu, x, wp, s, z, g, qt, path=None, **kw):
         taken = mn.last_path()
     finally:
         mn.set_option("force_path", 0)
-    return y, taken
+    return y, FAMILY.get(taken, taken) if path else taken
 
 
 def expect_path(path, taken, shape_ok=True):
@@ -182,8 +205,22 @@ def test_epilogues(mn, gpu, path, M):
     x, wp, s, z = O.make_int4_problem(M, K, N, g, seed=M + 11)
     acc = O.matmul_f32acc(x, O.dequant_int4(wp, s, z, K, g))
     b = np.random.default_rng(M).standard_normal(N).astype(np.float16)
-    y, taken = run_dm(mn, gpu, x, wp, s, z, g, "int4", path, epilogue="bias", bias=dev(b, gpu))
-    check_close(y, acc + b.astype(np.float32), f"bias [{taken}]")
+    bias = dev(b, gpu)
+    for epi in ("bias", "bias_relu", "bias_silu"):
+        y, taken = run_dm(mn, gpu, x, wp, s, z, g, "int4", path, epilogue=epi, bias=bias)
+        check_epilogue(y, acc, epi, f"{epi} [{taken}]", bias=b)
+    res = np.random.default_rng(M + 1).standard_normal((M, N)).astype(np.float16)
+    y, taken = run_dm(mn, gpu, x, wp, s, z, g, "int4", path, epilogue="residual", residual=dev(res, gpu))
+    check_epilogue(y, acc, "residual", f"residual [{taken}]", residual=res)
+    # in place: the residual is the output buffer
+    buf = dev(res, gpu)
+    mn.set_option("force_path", PATHS[path] if path else 0)
+    try:
+        mn.dequant_matmul(dev(x, gpu), dev(wp, gpu), dev(s, gpu), dev(z, gpu), g, "int4", epilogue="residual",
+                          residual=buf, out=buf)
+    finally:
+        mn.set_option("force_path", 0)
+    check_epilogue(host(buf), acc, "residual", f"residual in place [{mn.last_path()}]", residual=res)
     y, taken = run_dm(mn, gpu, x, wp, s, z, g, "int4", path, epilogue="swiglu")
     check_swiglu(y, acc, f"swiglu [{taken}]")
 
@@ -203,7 +240,7 @@ def test_config2_qwen7b_down(mn, gpu, M):
         if path == "rows" and taken != "rows":
             continue  # activations do not fit in LDS at this M
         assert taken == path
-        check_close(y, ref, f"config2 M={M} [{path}]")
+        check_close(y, ref, f"config2 M={M} [{path}, {mn.last_path()}]")
 
 
 def test_config1_qwen05b_gate(mn, gpu):
@@ -220,7 +257,7 @@ def test_config3_llama3b_qkv_prefill(mn, gpu):
     x, wp, s, z = O.make_int4_problem(M, K, N, g, seed=0)
     ref = O.matmul_f32acc(x, O.dequant_int4(wp, s, z, K, g))
     y, taken = run_dm(mn, gpu, x, wp, s, z, g, "int4")
-    assert taken == "tiled"
+    assert taken == "gemmw"
     check_close(y, ref, "config3")
 
 
@@ -235,7 +272,7 @@ def test_config4_int8_swiglu(mn, gpu, M):
         if path == "rows" and taken != "rows":
             continue  # activations do not fit in LDS at this M
         assert y.shape == (M, F) and taken == path
-        check_swiglu(y, acc, f"config4 M={M} [{path}]")
+        check_swiglu(y, acc, f"config4 M={M} [{path}, {mn.last_path()}]")
 
 
 # ---------------------------------------------------------------------------
@@ -562,33 +599,45 @@ def test_rows_kernel_ragged_runs(mn, gpu, M, K, N, g, qt, epi):
 
 
 @pytest.mark.parametrize("impl", [0, 1])
-@pytest.mark.parametrize("qt,epi", [("int4", None), ("int4", "bias"), ("int4", "swiglu"),
-                                    ("int8", None), ("int8", "swiglu")])
-@pytest.mark.parametrize("M,K,N", [(17, 256, 96), (100, 512, 320), (200, 1024, 256), (512, 768, 1056)])
-def test_prefill_gemm_kernels(mn, gpu, impl, qt, epi, M, K, N):
-    """Both prefill GEMM kernels (register-B, impl 0; LDS-staged, impl 1) on
-    ragged M / N tails, int4 g128 and int8 per-channel, each epilogue."""
-    say(f"gemm impl={impl} {qt} {epi} M={M} K={K} N={N}")
+@pytest.mark.parametrize("qt,g,epi", [("int4", 128, None), ("int4", 128, "bias"), ("int4", 128, "swiglu"),
+                                      ("int4", 64, None), ("int4", 32, "bias_silu"), ("int4", 64, "swiglu"),
+                                      ("int8", 0, None), ("int8", 0, "swiglu"), ("int8", 64, "residual")])
+@pytest.mark.parametrize("M,K,N", [(17, 256, 96), (100, 512, 320), (200, 1056, 256), (512, 768, 1056),
+                                   (130, 96, 80)])
+def test_prefill_gemm_kernels(mn, gpu, impl, qt, g, epi, M, K, N):
+    """The prefill GEMM kernels (impl 0: register-operand 32x32x16 kernel;
+    impl 1: 16x16x32 tiled kernel) on ragged M / N tails, K % 64 == 32, int4
+    with groups of 32, 64 and 128, int8 per-channel (g = 0) or grouped, and
+    the epilogues.  The kernel that ran is checked by name."""
+    say(f"gemm impl={impl} {qt} g={g} {epi} M={M} K={K} N={N}")
     if qt == "int4":
-        x, wp, s, z = O.make_int4_problem(M, K, N, 128, seed=M + K + N)
-        g = 128
+        x, wp, s, z = O.make_int4_problem(M, K, N, g, seed=M + K + N)
         acc = O.matmul_f32acc(x, O.dequant_int4(wp, s, z, K, g))
     else:
-        x, wp, s, z, g = O.make_int8_problem(M, K, N, seed=M + K + N)
+        x, wp, s, z, g = O.make_int8_problem(M, K, N, seed=M + K + N, g=g or None)
+        if epi == "residual":   # exercise the zero term of int8 too
+            z = np.random.default_rng(3).uniform(-0.01, 0.01, s.shape).astype(np.float16)
         acc = O.matmul_f32acc(x, O.dequant_int8(wp, s, z, K, g))
-    kw = {}
-    if epi == "bias":
+    kw, b, res = {}, None, None
+    if epi in ("bias", "bias_silu"):
         b = np.random.default_rng(N).standard_normal(N).astype(np.float16)
-        kw = {"epilogue": "bias", "bias": dev(b, gpu)}
+        kw = {"epilogue": epi, "bias": dev(b, gpu)}
+    elif epi == "residual":
+        res = np.random.default_rng(M).standard_normal((M, N)).astype(np.float16)
+        kw = {"epilogue": "residual", "residual": dev(res, gpu)}
     elif epi == "swiglu":
         kw = {"epilogue": "swiglu"}
     mn.set_option("gemm_impl", impl)
     try:
         y, taken = run_dm(mn, gpu, x, wp, s, z, g, qt, "tiled", **kw)
+        ran = mn.last_path()
     finally:
         mn.set_option("gemm_impl", 0)
     assert taken == "tiled"
+    assert ran == ("gemmw" if impl == 0 else "tiled"), ran
     if epi == "swiglu":
         check_swiglu(y, acc, f"gemm impl={impl}")
+    elif epi is None:
+        check_close(y, acc, f"gemm impl={impl}")
     else:
-        check_close(y, acc + b.astype(np.float32) if epi == "bias" else acc, f"gemm impl={impl}")
+        check_epilogue(y, acc, epi, f"gemm impl={impl} {epi}", bias=b, residual=res)
