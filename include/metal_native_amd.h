@@ -87,6 +87,23 @@ MQ_API int mq_dequant_matmul(const void* activations, int64_t lda, const void* w
                              int32_t quant_type, int32_t epilogue, const void* bias, const void* residual,
                              int64_t ldr, void* stream);
 
+/* mq_dequant_matmul that allocates nothing: no reference counterpart; for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  Same arguments,
+ * contract and kernels as mq_dequant_matmul; where the split-K decode GEMV
+ * runs, its counters and partial sums live in a fixed 8 MiB device array of
+ * the library (one per GPU, held until the process ends) instead of the
+ * per-stream workspace.  A shape whose split-K partials need more than that
+ * returns MQ_INVALID_ARGUMENT with the sizes in mq_last_error().  The first
+ * call on a device clears the array's counters with a kernel on the given
+ * stream; every call leaves them zero.  Calls that overlap on one GPU share
+ * the array and race: keep them stream-ordered. */
+MQ_API int mq_dequant_matmul_noalloc(const void* activations, int64_t lda, const void* weights_packed,
+                                     int64_t ldw_bytes, const void* scales, const void* zeros, void* out,
+                                     int64_t ldc, int64_t M, int64_t N, int64_t K, int32_t group_size,
+                                     int32_t quant_type, int32_t epilogue, const void* bias, const void* residual,
+                                     int64_t ldr, void* stream);
+
 /* Dequantize to fp16 out[N, K] (row stride ldo elements).
  * flat_groups == 0: per-row groups scales[n, k/g], optional zeros (NULL = no
  *   zero term) -- the fused kernels' dequant (matmul_dequant_kernel.metal:128-162).

@@ -131,7 +131,9 @@ int choose_path(const mq::LinearArgs& a) {
   return PATH_GENERIC;
 }
 
-int run_linear(const mq::LinearArgs& a, hipStream_t s) {
+// noalloc: the split-K GEMV uses the library's fixed scratch array instead of
+// the per-stream workspace (no allocation on any path).
+int run_linear(const mq::LinearArgs& a, hipStream_t s, bool noalloc = false) {
   int path = choose_path(a);
   hipError_t e;
   if (path == PATH_ROWS) {
@@ -139,11 +141,22 @@ int run_linear(const mq::LinearArgs& a, hipStream_t s) {
   } else if (path == PATH_DECODE) {
     const mq::GemvPlan pl = mq::gemv_plan(a, num_cus_current(), gemv_tuning());
     void* ws = nullptr;
-    e = workspace_for(s, pl.ws_bytes, &ws);
-    if (e == hipErrorStreamCaptureUnsupported)
-      return fail(MQ_INVALID_ARGUMENT, "dequant_matmul: the split-K workspace of this stream is too small; "
-                                       "make one call of this shape on the stream before capturing it");
-    if (e != hipSuccess) return hip_fail(e, "dequant_matmul: workspace allocation failed");
+    if (noalloc) {
+      if (pl.ws_bytes > mq::gemv_scratch_bytes())
+        return fail(MQ_INVALID_ARGUMENT, "dequant_matmul_noalloc: the split-K partial sums of this shape need " +
+                                             std::to_string(pl.ws_bytes) + " bytes, more than the fixed scratch of " +
+                                             std::to_string(mq::gemv_scratch_bytes()) + " bytes");
+      if (pl.ws_bytes) {
+        e = mq::gemv_scratch(s, &ws);
+        if (e != hipSuccess) return hip_fail(e, "dequant_matmul_noalloc: scratch set-up failed");
+      }
+    } else {
+      e = workspace_for(s, pl.ws_bytes, &ws);
+      if (e == hipErrorStreamCaptureUnsupported)
+        return fail(MQ_INVALID_ARGUMENT, "dequant_matmul: the split-K workspace of this stream is too small; "
+                                         "make one call of this shape on the stream before capturing it");
+      if (e != hipSuccess) return hip_fail(e, "dequant_matmul: workspace allocation failed");
+    }
     e = mq::gemv_launch(a, pl, ws, s);
   } else if (path == PATH_TILED) {
     const int impl = g_gemm_impl.load();
@@ -220,7 +233,7 @@ hipError_t allow_dynamic_lds(const void* kernel, int bytes) {
 
 extern "C" {
 
-MQ_API int mq_dequant_matmul(const void* activations, int64_t lda, const void* weights_packed,
+static int dequant_matmul_impl(bool noalloc, const void* activations, int64_t lda, const void* weights_packed,
                              int64_t ldw_bytes, const void* scales, const void* zeros, void* out,
                              int64_t ldc, int64_t M, int64_t N, int64_t K, int32_t group_size,
                              int32_t quant_type, int32_t epilogue, const void* bias, const void* residual,
@@ -251,7 +264,25 @@ MQ_API int mq_dequant_matmul(const void* activations, int64_t lda, const void* w
   a.scales = scales; a.zeros = zeros; a.bias = bias;
   a.resid = residual; a.ldr = ldr;
   a.C = out; a.ldc = ldc;
-  return run_linear(a, (hipStream_t)stream);
+  return run_linear(a, (hipStream_t)stream, noalloc);
+}
+
+MQ_API int mq_dequant_matmul(const void* activations, int64_t lda, const void* weights_packed,
+                             int64_t ldw_bytes, const void* scales, const void* zeros, void* out,
+                             int64_t ldc, int64_t M, int64_t N, int64_t K, int32_t group_size,
+                             int32_t quant_type, int32_t epilogue, const void* bias, const void* residual,
+                             int64_t ldr, void* stream) {
+  return dequant_matmul_impl(false, activations, lda, weights_packed, ldw_bytes, scales, zeros, out, ldc, M, N, K,
+                             group_size, quant_type, epilogue, bias, residual, ldr, stream);
+}
+
+MQ_API int mq_dequant_matmul_noalloc(const void* activations, int64_t lda, const void* weights_packed,
+                                     int64_t ldw_bytes, const void* scales, const void* zeros, void* out,
+                                     int64_t ldc, int64_t M, int64_t N, int64_t K, int32_t group_size,
+                                     int32_t quant_type, int32_t epilogue, const void* bias, const void* residual,
+                                     int64_t ldr, void* stream) {
+  return dequant_matmul_impl(true, activations, lda, weights_packed, ldw_bytes, scales, zeros, out, ldc, M, N, K,
+                             group_size, quant_type, epilogue, bias, residual, ldr, stream);
 }
 
 MQ_API int mq_rmsnorm_dequant_matmul(const void* x, const void* delta, const void* norm_weight, float eps,

@@ -38,6 +38,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <mutex>
 
 namespace mq {
 namespace {
@@ -469,6 +470,45 @@ GemvPlan gemv_plan(const LinearArgs& a, int num_cus, const GemvTuning& tu) {
     p.ws_bytes = p.cnt_bytes + (size_t)p.P * a.M * p.T * p.rpw * 4;
   }
   return p;
+}
+
+// ---- fixed scratch (mq_dequant_matmul_noalloc) ----
+// Device memory of the split-K counters and partials for callers that cannot
+// allocate.  In host code `scratch` names a host-side stand-in, not a device
+// address: every use goes through the per-device address from
+// hipGetSymbolAddress.  Calls that overlap on one GPU share it and race.
+constexpr size_t kScratchBytes = (size_t)8 << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+__global__ __launch_bounds__(256) void clear_words_kernel(uint32_t* p, int n) {
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) p[i] = 0u;
+}
+
+size_t gemv_scratch_bytes() { return kScratchBytes; }
+
+hipError_t gemv_scratch(hipStream_t s, void** out) {
+  static std::mutex mu;
+  static void* addr[64] = {};
+  *out = nullptr;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lk(mu);
+  if (!addr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    if (!p) return hipErrorInvalidSymbol;
+    // the counters start at zero (every launch leaves them zero again); a
+    // fill kernel, not a memset, so that a capturing caller records a kernel
+    hipLaunchKernelGGL(clear_words_kernel, dim3(64), dim3(256), 0, s, (uint32_t*)p, (int)(kCntBytes / 4));
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    addr[dev] = p;
+  }
+  *out = addr[dev];
+  return hipSuccess;
 }
 
 hipError_t gemv_launch(const LinearArgs& a, const GemvPlan& pl, void* ws, hipStream_t s) {

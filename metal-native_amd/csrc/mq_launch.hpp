@@ -77,6 +77,12 @@ GemvPlan gemv_plan(const LinearArgs& a, int num_cus, const GemvTuning& t);
 // ws: ws_bytes of device memory whose first cnt_bytes are zero (the kernel
 // leaves them zero again); calls sharing a workspace must be stream-ordered.
 hipError_t gemv_launch(const LinearArgs& a, const GemvPlan& p, void* ws, hipStream_t s);
+// Fixed split-K scratch for callers that cannot allocate: a file-scope
+// device array of gemv_scratch_bytes() bytes.  gemv_scratch returns its
+// address on the current device; the first call on a device looks the
+// symbol up and clears its counters with a kernel on stream s.
+size_t gemv_scratch_bytes();
+hipError_t gemv_scratch(hipStream_t s, void** ptr);
 
 // Persistent row-block GEMV (decode with the activations resident in LDS).
 struct RowsPlan {

@@ -42,6 +42,9 @@ SIGNATURES = {
     "mq_dequant_matmul": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p,
                                  _i64, _i64, _i64, _i64, _i32, _i32, _i32, _c_void_p, _c_void_p, _i64,
                                  _c_void_p]),
+    "mq_dequant_matmul_noalloc": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p,
+                                         _i64, _i64, _i64, _i64, _i32, _i32, _i32, _c_void_p, _c_void_p, _i64,
+                                         _c_void_p]),
     "mq_dequantize": (_i32, [_c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64,
                              _i32, _i32, _i32, _c_void_p]),
     "mq_rmsnorm_dequant_matmul": (_i32, [_c_void_p, _c_void_p, _c_void_p, ctypes.c_float, _c_void_p, _c_void_p,
