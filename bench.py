@@ -16,8 +16,9 @@ Method:
 * the launches are captured in a HIP graph (host launch overhead excluded),
   the graph is replayed, and HIP events on the replay stream bracket the
   timed region, with a device synchronisation on both sides;
-* the CPU baseline is the oracle's restatement (numpy dequantize + fp32 BLAS
-  matmul) timed on this host on the same workload (median of a few runs).
+* the CPU baseline is the reference's path restated on this host: torch-CPU
+  exact fp16 dequantize, then fp32 torch.matmul (warm-up 5, median of 20),
+  on the same workload, with the core count and CPU model stated.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only NAME]
 """
@@ -127,36 +128,36 @@ def measure(name, steps, warmup, device):
     x = torch.randn((M, K), device=device, generator=gen).half()
     fn = lambda i: mn.dequant_matmul(x, *weights[i % copies], g, qtype, epilogue=epi)
 
-    # graph of L launches cycling through the copies
-    L = copies * max(1, -(-64 // copies)) if copies < 64 else copies
+    # two graphs cycling through the copies: `warmup` untimed launches, then
+    # exactly `steps` timed ones
     stream = torch.cuda.Stream(device)
     stream.wait_stream(torch.cuda.current_stream(device))
     with torch.cuda.stream(stream):
         for i in range(copies):
-            fn(i)  # eager warm-up: workspace for this stream, code objects loaded
+            fn(i)  # eager: workspace for this stream, code objects loaded
     torch.cuda.synchronize(device)
     path = mn.last_path()
+    gwarm = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gwarm, stream=stream):
+        for i in range(max(1, warmup)):
+            fn(i)
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=stream):
-        for i in range(L):
+        for i in range(steps):
             fn(i)
-    reps = max(1, -(-steps // L))
-    wreps = max(1, -(-warmup // L))
     cur = torch.cuda.current_stream(device)
-    for _ in range(wreps):
-        graph.replay()
+    gwarm.replay()
     torch.cuda.synchronize(device)
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
     wall0 = time.perf_counter()
     t0.record(cur)
-    for _ in range(reps):
-        graph.replay()
+    graph.replay()
     t1.record(cur)
     torch.cuda.synchronize(device)
     wall = time.perf_counter() - wall0
     ms = t0.elapsed_time(t1)
-    n_steps = reps * L
+    n_steps = steps
     us_per_step = ms * 1000.0 / n_steps
     gbs = per_copy / (us_per_step * 1e-6) / 1e9
     res = {
@@ -176,7 +177,7 @@ def measure(name, steps, warmup, device):
     res["TFLOP/s"] = round(tf, 2)
     res["pct_fp16_mfma_peak"] = round(100 * tf / FP16_MFMA_PEAK_TFLOPS, 2)
     res["output_shape"] = [M, n_out]
-    del graph
+    del graph, gwarm
     del weights
     torch.cuda.empty_cache()
     return res
@@ -267,43 +268,78 @@ def prep_bench(device, reps: int = 50):
 # CPU baseline: the oracle on this host
 # --------------------------------------------------------------------------
 
-def cpu_baseline(reps: int = 10):
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(warmup: int = 5, reps: int = 20):
+    """The reference's path restated on this host (it has no CPU dequant):
+    torch-CPU dequantize with the exact two-rounding fp16 formula, then
+    ``torch.matmul(x.float(), W.float().T).half()``, timed with warm-up 5 and
+    median of 20 (README.md:86-90 method), at the full headline problem.
+    Threads: os.cpu_count() capped by OMP_NUM_THREADS (the GPU box grants one
+    GPU's share of its cores).  The oracle checks the dequantized weights."""
     import numpy as np
+    import torch
 
     from oracle import mq_oracle as O
 
-    try:
-        from threadpoolctl import threadpool_info
-
-        blas_threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
-    except Exception:  # noqa: BLE001
-        blas_threads = os.cpu_count() or 1
+    ncpu = os.cpu_count() or 1
+    threads = min(ncpu, int(os.environ.get("OMP_NUM_THREADS", ncpu) or ncpu))
+    torch.set_num_threads(threads)
     qtype, M, K, N, g, epi, _ = CONFIGS[HEADLINE]
     x, wp, s, z = O.make_int4_problem(M, K, N, g, seed=0)
-    times_dq, times_mm = [], []
-    for r in range(reps + 1):
+    xt = torch.from_numpy(x)
+    wpt = torch.from_numpy(wp)
+    st = torch.from_numpy(s)
+    zt = torch.from_numpy(z)
+
+    def dequant():
+        q = torch.stack([(wpt & 15), (wpt >> 4)], dim=-1).reshape(N, K).to(torch.int16)
+        sx = st.repeat_interleave(g, dim=1)[:, :K]
+        zx = zt.repeat_interleave(g, dim=1)[:, :K]
+        return (q - 8).half() * sx - zx   # two fp16 roundings, as the reference kernel
+
+    w = dequant()
+    if not np.array_equal(w.numpy().view(np.uint16), O.dequant_int4(wp, s, z, K, g).view(np.uint16)):
+        raise AssertionError("cpu baseline: torch-CPU dequant differs from the oracle")
+    td, tm = [], []
+    for r in range(warmup + reps):
         t0 = time.perf_counter()
-        w = O.dequant_int4(wp, s, z, K, g)
+        w = dequant()
         t1 = time.perf_counter()
-        y = O.matmul_f32acc(x, w).astype(np.float16)
+        y = torch.matmul(xt.float(), w.float().t()).half()
         t2 = time.perf_counter()
-        if r:  # first run is warm-up
-            times_dq.append(t1 - t0)
-            times_mm.append(t2 - t1)
-    dq, mm = float(np.median(times_dq)), float(np.median(times_mm))
+        if r >= warmup:
+            td.append(t1 - t0)
+            tm.append(t2 - t1)
+    dq, mm = float(np.median(td)), float(np.median(tm))
     total = dq + mm
     by = algo_bytes(qtype, M, K, N, g, epi)
+    fl = flops(M, K, N)
     del y
     return {
         "value": round(by / total / 1e9, 3),
         "unit": "GB/s",
-        "cores": blas_threads,
+        "cores": threads,
         "kind": "port",
-        "sample": (f"{HEADLINE} full problem (M={M},K={K},N={N},g={g}) on the host: oracle numpy "
-                   f"dequantize (single-threaded) then fp32 BLAS matmul ({blas_threads} threads) and fp16 "
-                   f"round; median of {reps} runs after 1 warm-up; dequant {dq*1e3:.1f} ms + matmul "
-                   f"{mm*1e3:.1f} ms"),
+        "sample": (f"{HEADLINE} full problem (M={M},K={K},N={N},g={g}) on the host ({_cpu_model()}, "
+                   f"os.cpu_count()={ncpu}, torch threads={threads}): torch-CPU exact fp16 dequantize, then "
+                   f"fp32 torch.matmul and fp16 round; median of {reps} after {warmup} warm-up; dequant "
+                   f"{dq*1e3:.1f} ms + matmul {mm*1e3:.1f} ms"),
         "ms_per_step": round(total * 1e3, 2),
+        "dequant_ms": round(dq * 1e3, 2),
+        "matmul_ms": round(mm * 1e3, 2),
+        "GFLOP/s": round(fl / total / 1e9, 2),
+        "cpu_model": _cpu_model(),
+        "os_cpu_count": ncpu,
     }
 
 
@@ -336,7 +372,7 @@ def main():
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--cpu-reps", type=int, default=10)
+    ap.add_argument("--cpu-reps", type=int, default=20)
     ap.add_argument("--only", default=None, help="comma-separated config names (headline always runs)")
     ap.add_argument("--only-headline", action="store_true", help="measure the headline config only")
     ap.add_argument("--decode-only", action="store_true",
@@ -394,7 +430,7 @@ def main():
     cpu = None
     if not args.no_cpu:
         log("[bench] cpu baseline ...")
-        cpu = cpu_baseline(args.cpu_reps)
+        cpu = cpu_baseline(5, args.cpu_reps)
         log(f"[bench] cpu: {json.dumps(cpu)}")
 
     achieved = head["GB/s"]

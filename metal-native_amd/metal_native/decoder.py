@@ -189,23 +189,30 @@ class SyntheticDecoder:
         ops.argmax_embed(logits, self.embed, token, pos, self.x0, self.tail_ws)
         return logits
 
-    def reference_step(self, token: int, pos: int, dequant) -> torch.Tensor:
+    def reference_step(self, token: int, pos: int, dequant, probe=None) -> torch.Tensor:
         """The same step in fp32 torch with weights from ``dequant(qlinear) ->
         fp16 [N, K]`` (e.g. the CPU oracle); returns logits [vocab] (fp32).
         Rounds to fp16 where the kernel path does (projection outputs,
-        residual stream, norms), so the two agree within the matmul tolerance."""
+        residual stream, norms), so the two agree within the matmul tolerance.
+        ``probe(name, layer, qlinear, x, y)``, when given, sees every linear's
+        fp16 input and fp32 output (bias included) of the reference chain."""
         cfg = self.cfg
         H, KVH, Dh = cfg.heads, cfg.kv_heads, cfg.head_dim
         grp = H // KVH
         dev = self.device
-        lin = lambda ql, x: (x.float() @ dequant(ql).to(dev).float().t())
+        def lin(ql, x, name="", li=-1):
+            y = x.float() @ dequant(ql).to(dev).float().t()
+            if probe is not None:
+                probe(name, li, ql, x, y + (ql.bias.float() if name == "qkv" else 0.0))
+            return y
+
         x = self.embed[token:token + 1]
         cos, sin = self.cos[pos], self.sin[pos]
         scale = 1.0 / math.sqrt(Dh)
         kv = self.kv.clone()
         for li, L in enumerate(self.layers):
             h = rms_norm(x, L["ln1"], cfg.eps)
-            qkv = (lin(L["qkv"], h) + L["qkv"].bias.float()).half()[0]
+            qkv = (lin(L["qkv"], h, "qkv", li) + L["qkv"].bias.float()).half()[0]
             q = apply_rope(qkv[:H * Dh].view(H, Dh), cos, sin)
             k = apply_rope(qkv[H * Dh:(H + KVH) * Dh].view(KVH, Dh), cos, sin)
             v = qkv[(H + KVH) * Dh:].view(KVH, Dh)
@@ -214,13 +221,13 @@ class SyntheticDecoder:
             kc, vc = kv[li, 0, :, :pos + 1].float(), kv[li, 1, :, :pos + 1].float()
             s = torch.matmul(q.view(KVH, grp, Dh).float(), kc.transpose(1, 2)) * scale
             a = torch.matmul(torch.softmax(s, dim=-1), vc).half().reshape(1, H * Dh)
-            x = x + lin(L["o"], a).half()
+            x = x + lin(L["o"], a, "o", li).half()
             h = rms_norm(x, L["ln2"], cfg.eps)
-            gu = lin(L["gate_up"], h).half().float()
+            gu = lin(L["gate_up"], h, "gate_up", li).half().float()
             gate, up = gu[:, :cfg.ffn], gu[:, cfg.ffn:]
             act = (gate / (1.0 + torch.exp(-gate)) * up).half()
-            x = x + lin(L["down"], act).half()
-        return lin(self.lm_head, rms_norm(x, self.norm, cfg.eps))[0]
+            x = x + lin(L["down"], act, "down", li).half()
+        return lin(self.lm_head, rms_norm(x, self.norm, cfg.eps), "lm_head")[0]
 
 
 def decode_tokens_per_second(model: SyntheticDecoder, n_tokens: int = 64, warmup: int = 3) -> dict:

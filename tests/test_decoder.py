@@ -2,7 +2,8 @@
 
 A tiny configuration is checked against an fp32 torch reference whose weights
 are dequantized by the CPU oracle (one decode step: logits within the matmul
-tolerance); HIP-graph replay must give the same tokens as eager steps.
+tolerance); HIP-graph replay must give the same tokens as eager steps.  The
+full 28-layer configuration is tests/test_decoder_full.py.
 """
 
 import numpy as np
@@ -38,7 +39,7 @@ def test_decode_step_matches_oracle_reference(gpu):
     torch.cuda.synchronize()
     got = logits[0].float()
     err = (got - ref).abs()
-    bound = 1e-2 + 1e-2 * ref.abs()
+    bound = 1e-2 + 1e-3 * ref.abs()   # the matmul contract
     assert bool((err <= bound).all()), f"max err {err.max().item():.3g}"
     # greedy choice agrees wherever the reference's top-2 margin exceeds the tolerance
     top2 = torch.topk(ref, 2).values
