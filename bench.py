@@ -77,6 +77,8 @@ CONFIGS = {
     "cfg2_qwen7b_down_m4": ("int4", 4, 18944, 3584, 128, None, "hbm"),
     "cfg2_qwen7b_down_m8": ("int4", 8, 18944, 3584, 128, None, "hbm"),
     "cfg3_llama3b_qkv_m512": ("int4", 512, 3072, 5120, 128, None, "mfma"),
+    "cfg3_llama3b_qkv_m512_g64": ("int4", 512, 3072, 5120, 64, None, "mfma"),
+    "cfg3_llama3b_qkv_m512_g32": ("int4", 512, 3072, 5120, 32, None, "mfma"),
     "cfg4_qwen7b_gateup_int8_swiglu_m1": ("int8", 1, 3584, 2 * 18944, 3584, "swiglu", "hbm"),
     "cfg4_qwen7b_gateup_int8_swiglu_m16": ("int8", 16, 3584, 2 * 18944, 3584, "swiglu", "hbm"),
     "cfg4_qwen7b_gateup_int8_swiglu_m64": ("int8", 64, 3584, 2 * 18944, 3584, "swiglu", "hbm"),

@@ -156,11 +156,13 @@ __device__ __forceinline__ f4 mfma16x16x32(h8 a, h8 b, f4 c) {
 
 // Read-out fence for MFMA accumulators: 24 wait states with the accumulator
 // as an in/out operand, so the MFMA that wrote it has retired before any
-// VALU/LDS/VMEM instruction reads it.  The compiler pads a VALU read of a
-// v_mfma_f32_16x16x32_f16 result on gfx950 with about 8 wait states, and
-// reads placed that close were measured to see stale upper accumulator
-// registers; every read-out of an MFMA result in this library goes through
-// this fence.
+// VALU/LDS/VMEM instruction reads it.  A guard, not a fix the current
+// compiler needs: an early split-K fold read stale upper accumulator
+// registers with the compiler's own padding (about 8 wait states after a
+// v_mfma_f32_16x16x32_f16), and the whole GPU test suite also passes with
+// this fence compiled out under ROCm 7.2 (clang 22).  It costs 24 cycles per
+// accumulator read-out (once per tile), and every read-out of an MFMA result
+// in this library goes through it (mq_gemmw.hip spells it with AGPR operands).
 __device__ __forceinline__ void mfma_result_fence(f4& v) {
   asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+v"(v));
 }
