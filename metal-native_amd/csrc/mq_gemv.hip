@@ -284,10 +284,14 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvKArgs p) {
   }
 
   // ---- split-K: partials, last-arriver reduction ----
-  // Partials and counters use system-scope (cache-coherent, L2-bypassing)
-  // accesses, so no L2 writeback or invalidate is needed anywhere: a
-  // workgroup's partial stores are complete (s_waitcnt) before its counter
-  // increment, and the elected workgroup reads them back coherently.
+  // Ordering: every access to the partials is a system-scope atomic (stores
+  // written through to memory, loads served from memory), and a workgroup's
+  // stores are acknowledged (s_waitcnt vmcnt(0)) before its counter
+  // increment.  That is the gfx942/gfx950 lowering of a system-scope release
+  // (and, on the reading side, acquire) minus the L2 writeback/invalidate,
+  // which exist only to publish non-atomic accesses; none are made here.
+  // The last workgroup to arrive sums the partials in split order; no
+  // workgroup ever waits for another.
   const int NP = p.T * RPW;
   if (holder && t < p.T) {  // tiles past T (last group) have no partial slots
 #pragma unroll

@@ -494,7 +494,10 @@ __global__ __launch_bounds__(256) void argmax_embed_kernel(const _Float16* logit
       if (am_better(sv[k], si[k], bv, bi)) { bv = sv[k]; bi = si[k]; }
     __hip_atomic_store(rv + blockIdx.x, bv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     __hip_atomic_store(ri + blockIdx.x, bi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-    // the record stores have completed before the arrival is counted
+    // the record stores (system-scope atomics, written through to memory)
+    // are acknowledged before the arrival is counted; the last arriver reads
+    // them with system-scope atomic loads: a release/acquire pair without
+    // the L2 writeback/invalidate, which only non-atomic accesses would need
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     s_arrived = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
   }
