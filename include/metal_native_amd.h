@@ -153,6 +153,14 @@ MQ_API int mq_quantize(const void* w, int64_t ldw, void* weights_packed, int64_t
 MQ_API int mq_vecmat_f16(const void* a, int64_t lda, const void* b, int64_t ldb, void* c, int64_t ldc,
                          int64_t M, int64_t N, int64_t K, int32_t transpose_b, void* stream);
 
+/* fp32 matmul route for skinny A: C[M,N] = A[M,K] . op(B), all fp32 (any M;
+ * rows of A in launches of 8).  Replaces matmul_vecmat_fp32 and
+ * matmul_vecmat_batch_fp32 (shaders/matmul_vecmat_kernel.metal:286-369,
+ * :462-534, selected at src/ops/matmul.mm:213-225) following the documented
+ * contract C = A @ op(B), as mq_vecmat_f16.  Deterministic. */
+MQ_API int mq_vecmat_f32(const void* a, int64_t lda, const void* b, int64_t ldb, void* c, int64_t ldc,
+                         int64_t M, int64_t N, int64_t K, int32_t transpose_b, void* stream);
+
 /* out[i] = half(silu(float(gate[i])) * float(up[i])), i < n.
  * Replaces fast::swiglu (src/future/future_stubs.mm:61-101, bound as
  * _C.fast.swiglu at bindings/bind_ops.cpp:84-93). */
@@ -221,10 +229,10 @@ MQ_API int mq_argmax_embed_f16(const void* logits, int64_t vocab, const void* em
  * value. */
 MQ_API int mq_set_option(const char* key, int64_t value);
 
-/* Kernel the last successful mq_dequant_matmul / mq_vecmat_f16 call on this
- * thread launched: 2 16x16x32 tiled GEMM, 3 generic, 4 vecmat [K,N], 6
- * split-K decode GEMV, 7 row-block decode GEMV, 8 register-operand 32x32x16
- * GEMM. */
+/* Kernel the last successful mq_dequant_matmul / mq_vecmat_f16 /
+ * mq_vecmat_f32 call on this thread launched: 2 16x16x32 tiled GEMM, 3
+ * generic, 4 vecmat [K,N], 6 split-K decode GEMV, 7 row-block decode GEMV, 8
+ * 32x32x16 prefill GEMM, 9 fp32 vecmat. */
 MQ_API int mq_last_path(void);
 
 MQ_API const char* mq_last_error(void);

@@ -54,7 +54,7 @@ int num_cus_current() {
 // (the 16x16x32 fallback).
 enum Path {
   PATH_AUTO = 0, PATH_TILED = 2, PATH_GENERIC = 3, PATH_VECMAT_KN = 4, PATH_DECODE = 6, PATH_ROWS = 7,
-  PATH_GEMMW = 8
+  PATH_GEMMW = 8, PATH_VECMAT32 = 9
 };
 // prefill GEMM choice (gemm_impl): 0 the register-operand 32x32x16 kernel
 // where it takes the shape, 1 always the 16x16x32 tiled kernel
@@ -410,6 +410,20 @@ MQ_API int mq_vecmat_f16(const void* a, int64_t lda, const void* b, int64_t ldb,
   hipError_t e = mq::generic_linear_launch(la, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "matmul: kernel launch failed");
   g_last_path = PATH_GENERIC;
+  return MQ_SUCCESS;
+}
+
+MQ_API int mq_vecmat_f32(const void* a, int64_t lda, const void* b, int64_t ldb, void* c, int64_t ldc,
+                         int64_t M, int64_t N, int64_t K, int32_t transpose_b, void* stream) {
+  if (!a || !b || !c) return fail(MQ_INVALID_ARGUMENT, "matmul: null pointer argument");
+  if (M < 1 || N < 1 || K < 1 || M > INT32_MAX || N > INT32_MAX || K > INT32_MAX)
+    return fail(MQ_INVALID_ARGUMENT, "matmul: bad shape");
+  if (lda < K || ldc < N || ldb < (transpose_b ? K : N))
+    return fail(MQ_INVALID_ARGUMENT, "matmul: leading dimension too small");
+  hipError_t e = mq::vecmat32_launch(a, lda, b, ldb, c, ldc, (int)M, (int)N, (int)K, transpose_b != 0,
+                                     (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "matmul: kernel launch failed");
+  g_last_path = PATH_VECMAT32;
   return MQ_SUCCESS;
 }
 

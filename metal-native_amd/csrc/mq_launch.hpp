@@ -153,4 +153,8 @@ hipError_t swiglu_launch(const void* gate, const void* up, void* out, int64_t n,
 hipError_t vecmat_kn_launch(const void* A, int64_t lda, const void* B, int64_t ldb,
                             void* C, int64_t ldc, int M, int N, int K, hipStream_t s);
 
+// fp32 GEMV, any M (launches of 8 rows): C = A . B (B [K, N]) or A . B^T (B [N, K]).
+hipError_t vecmat32_launch(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc, int M,
+                           int N, int K, bool transpose_b, hipStream_t s);
+
 }  // namespace mq

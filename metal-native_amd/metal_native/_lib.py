@@ -31,7 +31,7 @@ EPILOGUE_BIAS_SILU = 3
 EPILOGUE_RESIDUAL = 4
 EPILOGUE_SWIGLU = 5
 
-PATH_NAMES = {0: "none", 2: "tiled", 3: "generic", 4: "vecmat_kn", 6: "decode", 7: "rows", 8: "gemmw"}
+PATH_NAMES = {0: "none", 2: "tiled", 3: "generic", 4: "vecmat_kn", 6: "decode", 7: "rows", 8: "gemmw", 9: "vecmat_f32"}
 
 _c_void_p = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -54,6 +54,8 @@ SIGNATURES = {
     "mq_quantize": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _c_void_p, _i64, _i64, _i32, _i32,
                            _c_void_p]),
     "mq_vecmat_f16": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _i64, _i64, _i64, _i64,
+                             _i32, _c_void_p]),
+    "mq_vecmat_f32": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _i64, _i64, _i64, _i64,
                              _i32, _c_void_p]),
     "mq_swiglu_f16": (_i32, [_c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p]),
     "mq_add_rmsnorm_f16": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, ctypes.c_float,

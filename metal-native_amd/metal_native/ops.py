@@ -324,14 +324,14 @@ def quantize(w: torch.Tensor, group_size: int, quant_type: str):
 def _vecmat_route(M: int, N: int, K: int, dtype: torch.dtype) -> bool:
     """select_kernel's VecMat condition (src/ops/matmul.mm:177-178), for the
     dtypes this build has a kernel for."""
-    return M <= 8 and N >= 256 and K >= 256 and dtype == torch.float16
+    return M <= 8 and N >= 256 and K >= 256 and dtype in (torch.float16, torch.float32)
 
 
 def matmul(a: torch.Tensor, b: torch.Tensor, transpose_a: bool = False,
            transpose_b: bool = False) -> torch.Tensor:
     """``_C.matmul``: ``a @ op(b)``.
 
-    The M<=8 fp16 route (the reference's vecmat kernels) runs on this
+    The M<=8 fp16 and fp32 routes (the reference's vecmat kernels) run on this
     library's kernels; ``b`` is ``[K, N]``, or ``[N, K]`` with ``transpose_b``
     (the documented contract, include/metal_native/ops/matmul.h:18-37).
     Shapes outside that route are the reference's non-quantized
@@ -366,15 +366,15 @@ def matmul(a: torch.Tensor, b: torch.Tensor, transpose_a: bool = False,
         b = b.contiguous()
     b, ldb = _rowmajor(b, "b", op)
     rows = a2.shape[0]
-    out = torch.empty((rows, N), dtype=torch.float16, device=a.device)
+    out = torch.empty((rows, N), dtype=a.dtype, device=a.device)
     dev = a.device
+    fn = _L.mq_vecmat_f16 if a.dtype == torch.float16 else _L.mq_vecmat_f32
     with torch.cuda.device(dev):
         for r0 in range(0, rows, 64):
             r1 = min(rows, r0 + 64)
             ai, lda = _rowmajor(a2[r0:r1], "a", op)
-            rc = _L.mq_vecmat_f16(_ptr(ai), lda, _ptr(b), ldb,
-                                  _ptr(out[r0:r1]), N, r1 - r0, N, K, 1 if transpose_b else 0,
-                                  _stream_handle(dev))
+            rc = fn(_ptr(ai), lda, _ptr(b), ldb, _ptr(out[r0:r1]), N, r1 - r0, N, K, 1 if transpose_b else 0,
+                    _stream_handle(dev))
             _check(rc)
     return out.reshape(*lead, M, N)
 

@@ -361,6 +361,55 @@ def test_vecmat_route(mn, gpu, M, K, N, transpose_b):
     check_close(got, ref, f"vecmat tb={transpose_b}")
 
 
+def check_f32(got, ref64, K, what):
+    """fp32 products: each output is a K-term fp32 sum; the bound is a few
+    fp32 roundings per term of the magnitudes summed (|a| . |b|)."""
+    err = np.abs(got.astype(np.float64) - ref64[0])
+    bound = 1e-6 + 4 * K * 2.0 ** -24 * ref64[1]
+    assert (err <= bound).all(), f"{what}: max err {err.max():.3g}, bound {bound.min():.3g}"
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 256, 256), (1, 4096, 4096), (3, 1000, 300), (8, 4100, 257),
+                                   (8, 262, 1024)])
+@pytest.mark.parametrize("transpose_b", [True, False])
+def test_vecmat_f32_route(mn, gpu, M, K, N, transpose_b):
+    """The fp32 vecmat route (matmul_vecmat_fp32 / _batch_fp32) on the library's kernel."""
+    say(f"vecmat f32 M={M} K={K} N={N} tb={transpose_b}")
+    rng = np.random.default_rng(M * K + N + 7)
+    a = rng.standard_normal((M, K)).astype(np.float32)
+    b = (rng.standard_normal((N, K) if transpose_b else (K, N)) * 0.05).astype(np.float32)
+    bt = (b.T if transpose_b else b).astype(np.float64)
+    ref = (a.astype(np.float64) @ bt, np.abs(a).astype(np.float64) @ np.abs(bt))
+    y = mn.matmul(dev(a, gpu), dev(b, gpu), False, transpose_b)
+    assert y.dtype == torch.float32 and mn.last_path() == "vecmat_f32"
+    got = host(y)
+    check_f32(got, ref, K, f"vecmat f32 tb={transpose_b}")
+    np.testing.assert_array_equal(host(mn.matmul(dev(a, gpu), dev(b, gpu), False, transpose_b)), got)
+
+
+@pytest.mark.parametrize("transpose_b", [True, False])
+def test_vecmat_f32_c_abi_strides(mn, gpu, transpose_b):
+    """mq_vecmat_f32 directly: M = 11 (two launches of rows), padded row strides."""
+    from metal_native import _lib as L
+
+    say(f"vecmat f32 C ABI tb={transpose_b}")
+    M, K, N = 11, 777, 300
+    rng = np.random.default_rng(5)
+    a = torch.from_numpy(rng.standard_normal((M, K + 5)).astype(np.float32)).to(gpu)
+    rb, cb = (N, K) if transpose_b else (K, N)
+    b = torch.from_numpy((rng.standard_normal((rb, cb + 3)) * 0.05).astype(np.float32)).to(gpu)
+    c = torch.full((M, N + 2), float("nan"), dtype=torch.float32, device=gpu)
+    rc = L.lib.mq_vecmat_f32(a.data_ptr(), K + 5, b.data_ptr(), cb + 3, c.data_ptr(), N + 2, M, N, K,
+                               1 if transpose_b else 0, torch.cuda.current_stream(gpu).cuda_stream)
+    assert rc == 0
+    an = host(a)[:, :K].astype(np.float64)
+    bn = host(b)[:, :cb].astype(np.float64)
+    bt = bn.T if transpose_b else bn
+    got = host(c)
+    check_f32(got[:, :N], (an @ bt, np.abs(an) @ np.abs(bt)), K, "vecmat f32 C ABI")
+    assert np.isnan(got[:, N:]).all()   # nothing written past N
+
+
 # ---------------------------------------------------------------------------
 # behaviour: determinism, row independence, repeated calls, graphs, errors
 # ---------------------------------------------------------------------------
