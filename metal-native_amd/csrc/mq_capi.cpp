@@ -125,7 +125,10 @@ int choose_path(const mq::LinearArgs& a) {
   if (forced == PATH_DECODE && decode_ok(a)) return PATH_DECODE;
   if (forced == PATH_TILED && prefill_ok(a)) return PATH_TILED;
   if (forced == PATH_GENERIC) return PATH_GENERIC;
-  if (rows_ok(a)) return PATH_ROWS;
+  // automatic choice: the row-block kernel up to M = 4 (its 8-row tiles for
+  // M = 5..8 measured slower than the split-K GEMV at config 2: 19.6 vs
+  // 18.0 us); forced, it takes M <= 8
+  if (a.M <= 4 && rows_ok(a)) return PATH_ROWS;
   if (decode_ok(a)) return PATH_DECODE;
   if (prefill_ok(a)) return PATH_TILED;
   return PATH_GENERIC;
@@ -135,9 +138,24 @@ int choose_path(const mq::LinearArgs& a) {
 // the per-stream workspace (no allocation on any path).
 int run_linear(const mq::LinearArgs& a, hipStream_t s, bool noalloc = false) {
   int path = choose_path(a);
-  hipError_t e;
+  hipError_t e = hipSuccess;
   if (path == PATH_ROWS) {
-    e = mq::rows_launch(a, mq::rows_plan(a, num_cus_current()), s);
+    // K parts need the workspace: the no-allocation entry point takes the
+    // split-K GEMV (whose scratch is fixed) for such shapes
+    const mq::RowsPlan pl = mq::rows_plan(a, num_cus_current(), !noalloc);
+    if (pl.ok) {
+      void* ws = nullptr;
+      e = workspace_for(s, pl.ws_bytes, &ws);
+      if (e == hipErrorStreamCaptureUnsupported)
+        return fail(MQ_INVALID_ARGUMENT, "dequant_matmul: the split-K workspace of this stream is too small; "
+                                         "make one call of this shape on the stream before capturing it");
+      if (e != hipSuccess) return hip_fail(e, "dequant_matmul: workspace allocation failed");
+      e = mq::rows_launch(a, pl, ws, s);
+    } else {
+      path = decode_ok(a) ? PATH_DECODE : PATH_GENERIC;
+    }
+  }
+  if (path == PATH_ROWS) {
   } else if (path == PATH_DECODE) {
     const mq::GemvPlan pl = mq::gemv_plan(a, num_cus_current(), gemv_tuning());
     void* ws = nullptr;
@@ -311,7 +329,7 @@ MQ_API int mq_rmsnorm_dequant_matmul(const void* x, const void* delta, const voi
     return fail(MQ_INVALID_ARGUMENT, "rmsnorm_dequant_matmul: weight rows too short");
   const mq::RowsPlan pl = mq::rows_plan(a, num_cus_current());
   if (!pl.ok) return fail(MQ_INVALID_ARGUMENT, "rmsnorm_dequant_matmul: shape not supported by the fused kernel");
-  hipError_t e = mq::rows_launch(a, pl, (hipStream_t)stream);
+  hipError_t e = mq::rows_launch(a, pl, nullptr, (hipStream_t)stream);   // pre-norm: one K part, no workspace
   if (e != hipSuccess) return hip_fail(e, "rmsnorm_dequant_matmul: kernel launch failed");
   g_last_path = PATH_ROWS;
   return MQ_SUCCESS;

@@ -85,14 +85,17 @@ size_t gemv_scratch_bytes();
 hipError_t gemv_scratch(hipStream_t s, void** ptr);
 
 // Persistent row-block GEMV (decode with the activations resident in LDS).
+// KP > 1 splits K into parts (activations too long for LDS); the parts of a
+// row block meet through ws_bytes of the per-stream workspace.
 struct RowsPlan {
   int rpw, nw, nwg, R, TW, KS, XS, maxT, szrows, szpad;
+  int KP, nblk, KStot;
   uint32_t off_sz, off_scr, off_slot;
-  size_t lds_bytes;
+  size_t lds_bytes, ws_bytes;
   bool ok;
 };
-RowsPlan rows_plan(const LinearArgs& a, int num_cus);
-hipError_t rows_launch(const LinearArgs& a, const RowsPlan& p, hipStream_t s);
+RowsPlan rows_plan(const LinearArgs& a, int num_cus, bool allow_split = true);
+hipError_t rows_launch(const LinearArgs& a, const RowsPlan& p, void* ws, hipStream_t s);
 
 // Register-operand 32x32x16 MFMA GEMM (prefill default).
 bool gemmw_supported(const LinearArgs& a, int num_cus);

@@ -6,15 +6,19 @@
 // src/ops/matmul.mm:946-1009; shaders/matmul_vecmat_kernel.metal:32-139 for
 // fp16 B [N, K]), computing every row of A.
 //
-// Structure (no synchronisation between workgroups, one launch):
+// Structure (one launch; no workgroup waits for another):
 //  * One workgroup of NW wavefronts per CU.  Workgroup b owns R consecutive
 //    output rows (SwiGLU: R output columns = R gate + R up weight rows) over
 //    the whole of K, so every CU streams the same number of weight bytes.
+//    When the activations of all of K do not fit in LDS (M = 4 at K = 18944),
+//    K is cut into KP contiguous parts: one workgroup per (row block, part),
+//    with KP times the rows, and the parts of a row block meet through the
+//    workspace (the last to arrive sums them in K order).
 //  * Row tile: RPW weight rows x S = 16/RPW K shifts form the 16 columns of the
 //    B operand of v_mfma_f32_16x16x32_f16; one wave load reads RPW rows x 64*S
 //    contiguous bytes.  The A operand holds activation row i % RPW at K shift
-//    i / RPW (needs M <= RPW); the result for (activation i, weight row r) is
-//    sum_s D[s*RPW + i][s*RPW + r].
+//    i / RPW (needs M <= RPW; RPW = 8 only for the quantized formats); the
+//    result for (activation i, weight row r) is sum_s D[s*RPW + i][s*RPW + r].
 //  * The workgroup's work is TW tiles x KS K-steps ("units", tile-major); wave
 //    w takes the contiguous units [w*U/NW, (w+1)*U/NW) and streams them
 //    through a ring of D register slots refilled as they are consumed.  Every
@@ -46,6 +50,7 @@ constexpr int kPre = 2;      // ring slots issued before the staging data is wai
 constexpr int kXB = 8;           // activation pieces per thread per staging batch
 constexpr int kSB = 2;           // scale/zero pieces per thread per staging batch
 constexpr size_t kLds = 163840;  // LDS per CU on gfx950
+constexpr size_t kCntBytesRows = 65536;   // workspace counters (the split-K GEMV's layout)
 
 struct RowsKArgs {
   const _Float16* A; int64_t lda;
@@ -56,7 +61,11 @@ struct RowsKArgs {
   int M, K, N, F, G, gshift;
   int R;          // output rows (SwiGLU: output columns) per workgroup
   int TW;         // row tiles per workgroup
-  int KS;         // K steps per row
+  int KS;         // K steps per part (staged width; the last part may have fewer)
+  int KStot;      // K steps per row
+  int KP, nblk;   // K parts, row blocks (grid = KP * nblk)
+  float* part;    // KP > 1: fp32 partial outputs [KP][nblk][M * R * (SwiGLU ? 2 : 1)]
+  uint32_t* cnt;  // KP > 1: arrivals per row block (zero between launches)
   int XS;         // LDS activation row stride (halves)
   int maxT;       // partial slots per wave
   int szrows;     // weight rows whose scales are staged (R, or 2R for SwiGLU)
@@ -82,8 +91,10 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
   constexpr int NT = 64 * kNW;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int M = p.M, KS = p.KS;
-  const int b = blockIdx.x;
+  // K part kpi of row block b: steps [ks0, ks0 + KS) of the row
+  const int kpi = blockIdx.x / p.nblk, b = blockIdx.x - kpi * p.nblk;
+  const int ks0 = kpi * p.KS;
+  const int M = p.M, KS = min(p.KStot - ks0, p.KS);
 
   _Float16* xs = (_Float16*)smem;                     // [M][XS]
   uint32_t* szl = (uint32_t*)(smem + p.off_sz);       // [szrows][G]: s | z << 16
@@ -146,12 +157,12 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
   // hold any bits); its lane part is lvo_last.  Quantized bytes past K (the
   // next row's, row padding, or zeros past the range) dequantize to finite
   // values that meet zero activations, so those lanes load unmasked.
-  const bool kpast = FMT == FMT_F16 && (KS - 1) * KSTEP + klane >= p.K;
+  const bool kpast = FMT == FMT_F16 && (ks0 + KS - 1) * KSTEP + klane >= p.K;
   uint32_t lvo = lane_off(lt), lvo_last = kpast ? kOobPart : lvo;
   auto wload = [&]() -> u4 {
     uint32_t so = kOobPart, vo = lvo;
     if (left > 0) {
-      so = (uint32_t)(lj * (KSTEP * BPK2 / 2));
+      so = (uint32_t)((ks0 + lj) * (KSTEP * BPK2 / 2));
       if (FMT == FMT_F16 && lj == KS - 1) vo = lvo_last;
       --left;
       if (++lj == KS) {
@@ -167,7 +178,8 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
   // ---- staging loads, issued before the ring: the load counter completes
   // in order, so staging data loaded after the ring would wait for it ----
   const rsrc_t ar = make_rsrc(p.A, p.a_bytes);
-  const int ppr = KS * KSTEP / 8;   // whole units: k past K is staged as zeros
+  const int ppr = p.KS * KSTEP / 8;   // whole units (the widest part): k past K is staged as zeros
+  const int kx0 = ks0 * KSTEP / 8;     // the part's first 16-byte piece of a row
   const int npieces = M * ppr;
   // exact batch sizes: every load instruction costs texture-unit time, even
   // one whose lanes are all out of range
@@ -178,7 +190,7 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
       if (e < cnt) {
         const int idx = base + tid + e * NT;
         const int i = M == 1 ? 0 : (int)(((uint64_t)(uint32_t)idx * p.ppr_magic) >> 32), c = idx - i * ppr;
-        v[e] = bload16(ar, (idx < npieces && 8 * c < p.K) ? (uint32_t)((i * p.lda + 8 * c) * 2) : kOob);
+        v[e] = bload16(ar, (idx < npieces && 8 * (kx0 + c) < p.K) ? (uint32_t)((i * p.lda + 8 * (kx0 + c)) * 2) : kOob);
       }
     }
   };
@@ -373,7 +385,7 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
   // the next row's: any finite scale, the weights there meet zero activations)
   const int sadv = p.gshift >= 31 ? 0 : (KSTEP >> p.gshift);
   const int sl = p.gshift >= 31 ? 0 : (klane >> p.gshift);
-  int sa = sz_row(ct) * G + sl + cj * sadv;
+  int sa = sz_row(ct) * G + sl + (ks0 + cj) * sadv;
   const _Float16* xa = xs + xrow + xswz(cj * KSTEP + klane);
   static_assert(KSTEP % 128 == 0, "the LDS activation padding advances by a constant per unit");
   constexpr int XADV = KSTEP + (KSTEP >> 7) * 8;
@@ -446,7 +458,7 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
             cj = 0;
             ++ct;
             xa = xs + xrow + xswz(klane);
-            sa = sz_row(ct) * G + sl;
+            sa = sz_row(ct) * G + sl + ks0 * sadv;
           }
         }
       }
@@ -466,6 +478,57 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
     }
     return v;
   };
+  if (p.KP > 1) {
+    // ---- K parts: partial outputs through the workspace; the last part of
+    // the row block to arrive sums them in K order ----
+    // Ordering: every access to the partials is a system-scope atomic
+    // (stores written through to memory, loads served from memory) and a
+    // workgroup's stores are acknowledged (s_waitcnt vmcnt(0)) before its
+    // arrival is counted: the release/acquire of the split-K GEMV's
+    // protocol.  No workgroup waits for another.
+    constexpr int PV = EPI == EPI_SWIGLU ? 2 : 1;
+    const int64_t pstride = (int64_t)p.nblk * M * p.R * PV;   // one part
+    float* const pown = p.part + (int64_t)kpi * pstride + (int64_t)b * M * p.R * PV;
+    auto own = [&](int idx, int e) -> float {   // this part's sum: output idx, gate (0) or up (1)
+      const int i = idx / valid, c = idx - i * valid;
+      if (EPI == EPI_SWIGLU) {
+        const int t = c / HALF, rr = c - t * HALF;
+        return tile_sum(t, i, rr + e * HALF);
+      }
+      const int t = c / RPW, rr = c - t * RPW;
+      return tile_sum(t, i, rr);
+    };
+    for (int idx = tid; idx < M * valid; idx += NT)
+#pragma unroll
+      for (int e = 0; e < PV; ++e)
+        __hip_atomic_store(pown + idx * PV + e, own(idx, e), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    // the arrival flag lives in the per-wave scratch (free since the last
+    // fold; a static __shared__ variable would shrink the dynamic LDS the
+    // kernel may request)
+    volatile uint32_t* s_last = (volatile uint32_t*)(smem + p.off_scr);
+    if (tid == 0)
+      *s_last = __hip_atomic_fetch_add(p.cnt + b, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) == (uint32_t)(p.KP - 1);
+    __syncthreads();
+    if (!*s_last) return;
+    for (int idx = tid; idx < M * valid; idx += NT) {
+      float v[PV];
+#pragma unroll
+      for (int e = 0; e < PV; ++e) {
+        v[e] = 0.f;
+        for (int kp = 0; kp < p.KP; ++kp)   // K order, whatever the arrival order
+          v[e] += kp == kpi ? own(idx, e) : ld_coherent(pown + (int64_t)(kp - kpi) * pstride + idx * PV + e);
+      }
+      const int i = idx / valid, c = idx - i * valid;
+      if (EPI == EPI_SWIGLU)
+        p.C[(int64_t)i * p.ldc + row0 + c] = (_Float16)(silu_f32((float)(_Float16)v[0]) * (float)(_Float16)v[PV - 1]);
+      else
+        p.C[(int64_t)i * p.ldc + row0 + c] = (_Float16)epi_apply(v[0], i, row0 + c, p.ep);
+    }
+    if (tid == 0) __hip_atomic_store(p.cnt + b, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    return;
+  }
   if (EPI == EPI_SWIGLU) {
     for (int idx = tid; idx < M * valid; idx += NT) {
       const int i = idx / valid, c = idx - i * valid;
@@ -506,6 +569,9 @@ hipError_t launch2(const RowsKArgs& k, const RowsPlan& pl, hipStream_t s) {
     case 1: return EPI == EPI_SWIGLU ? hipErrorInvalidValue : launch3<FMT, EPI, 1>(k, pl, s);
     case 2: return launch3<FMT, EPI, 2>(k, pl, s);
     case 4: return launch3<FMT, EPI, 4>(k, pl, s);
+    case 8:   // 8-row tiles: 2 K shifts, quantized formats only (an fp16 step would be 64 k)
+      if constexpr (FMT != FMT_F16) return launch3<FMT, EPI, 8>(k, pl, s);
+      return hipErrorInvalidValue;
     default: return hipErrorInvalidValue;
   }
 }
@@ -529,11 +595,13 @@ int szrows_of(const LinearArgs& a, int R) { return a.epi == EPI_SWIGLU ? 2 * R :
 
 }  // namespace
 
-RowsPlan rows_plan(const LinearArgs& a, int num_cus) {
+namespace {
+
+RowsPlan rows_plan_k(const LinearArgs& a, int num_cus, int KP) {
   RowsPlan p{};
   p.ok = false;
   const int kpl = kpl_of(a.fmt);
-  if (a.M < 1 || a.M > 4) return p;
+  if (a.M < 1 || a.M > (a.fmt == FMT_F16 ? 4 : 8)) return p;
   if (a.K % kpl != 0 || (a.K & 7)) return p;
   if (a.fmt != FMT_F16 && a.G != 1 && (gshift_of(a) < 0 || a.g < kpl)) return p;
   if (((uintptr_t)a.W & 15) || (a.ldw & 15)) return p;
@@ -548,7 +616,7 @@ RowsPlan rows_plan(const LinearArgs& a, int num_cus) {
   // workgroup rounded up to whole tiles, times K rounded up to whole steps
   int rpw = 4;
   double best_work = 1e300;
-  for (int cand = 1; cand <= 4; cand <<= 1) {
+  for (int cand = 1; cand <= (a.fmt == FMT_F16 ? 4 : 8); cand <<= 1) {
     if (cand < a.M || (a.epi == EPI_SWIGLU && cand < 2)) continue;
     const int ks = 4 * kpl * (16 / cand);
     const int gr = a.epi == EPI_SWIGLU ? cand / 2 : cand;
@@ -559,12 +627,16 @@ RowsPlan rows_plan(const LinearArgs& a, int num_cus) {
   const int S = 16 / rpw;
   const int kstep = 4 * kpl * S;
   const int gran = a.epi == EPI_SWIGLU ? rpw / 2 : rpw;  // output rows per tile
-  // rows per workgroup: a whole number of tiles, one workgroup per CU
-  int R = (nrows + num_cus - 1) / num_cus;
+  // rows per workgroup: a whole number of tiles, one workgroup (one K part
+  // of a row block) per CU
+  int R = (int)(((int64_t)nrows * KP + num_cus - 1) / num_cus);
   R = (R + gran - 1) / gran * gran;
-  const int nwg = (nrows + R - 1) / R;
+  const int nblk = (nrows + R - 1) / R;
+  const int nwg = nblk * KP;
   const int TW = R / gran;
-  const int KS = (a.K + kstep - 1) / kstep;
+  const int KStot = (a.K + kstep - 1) / kstep;
+  const int KS = (KStot + KP - 1) / KP;   // steps per part
+  if (KP > 1 && (int64_t)KS * (KP - 1) >= KStot) return p;   // every part has steps
   const int U = TW * KS;
   const int nw = kNW;
   const int per = (U + nw - 1) / nw;
@@ -598,6 +670,9 @@ RowsPlan rows_plan(const LinearArgs& a, int num_cus) {
     if (n_x * ppr >= (1ull << 32) || n_s * (uint64_t)a.G >= (1ull << 32)) return p;
   }
   p.rpw = rpw; p.nw = nw; p.nwg = nwg; p.R = R; p.TW = TW; p.KS = KS; p.XS = XS; p.maxT = maxT;
+  p.KP = KP; p.nblk = nblk; p.KStot = KStot;
+  p.ws_bytes = KP > 1 ? kCntBytesRows + (size_t)KP * nblk * a.M * R * (a.epi == EPI_SWIGLU ? 2 : 1) * 4 : 0;
+  if (KP > 1 && (size_t)nblk * 4 > kCntBytesRows) return p;
   p.szrows = szrows;
   p.szpad = szpad;
   p.lds_bytes = off;
@@ -605,8 +680,23 @@ RowsPlan rows_plan(const LinearArgs& a, int num_cus) {
   return p;
 }
 
-hipError_t rows_launch(const LinearArgs& a, const RowsPlan& pl, hipStream_t s) {
+}  // namespace
+
+RowsPlan rows_plan(const LinearArgs& a, int num_cus, bool allow_split) {
+  RowsPlan p{};
+  p.ok = false;
+  // K parts: the fewest whose activation slice fits in LDS (more rows per
+  // workgroup, so that the parts of all row blocks still cover the CUs once)
+  for (int kp = 1; kp <= (allow_split && !a.prenorm ? 4 : 1); ++kp) {
+    p = rows_plan_k(a, num_cus, kp);
+    if (p.ok) return p;
+  }
+  return p;
+}
+
+hipError_t rows_launch(const LinearArgs& a, const RowsPlan& pl, void* ws, hipStream_t s) {
   if (!pl.ok) return hipErrorInvalidValue;
+  if (pl.KP > 1 && !ws) return hipErrorInvalidValue;
   RowsKArgs k{};
   k.A = (const _Float16*)a.A; k.lda = a.lda;
   k.W = (const unsigned char*)a.W; k.ldw = a.ldw;
@@ -615,6 +705,11 @@ hipError_t rows_launch(const LinearArgs& a, const RowsPlan& pl, hipStream_t s) {
   k.C = (_Float16*)a.C; k.ldc = a.ldc;
   k.M = a.M; k.K = a.K; k.N = a.N; k.F = a.F; k.G = a.G;
   k.gshift = gshift_of(a);
+  k.KStot = pl.KStot; k.KP = pl.KP; k.nblk = pl.nblk;
+  if (pl.KP > 1) {
+    k.cnt = (uint32_t*)ws;
+    k.part = (float*)((char*)ws + kCntBytesRows);
+  }
   k.R = pl.R; k.TW = pl.TW; k.KS = pl.KS; k.XS = pl.XS; k.maxT = pl.maxT; k.szrows = pl.szrows; k.szpad = pl.szpad;
   k.off_sz = pl.off_sz; k.off_scr = pl.off_scr; k.off_slot = pl.off_slot;
   if (a.prenorm) {

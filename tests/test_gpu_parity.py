@@ -647,6 +647,53 @@ def test_rows_kernel_ragged_runs(mn, gpu, M, K, N, g, qt, epi):
         check_close(y, acc, "rows ragged")
 
 
+@pytest.mark.parametrize("M,K,N,g,qt,epi", [
+    (4, 18944, 3584, 128, "int4", None),     # config 2 at M = 4: two K parts
+    (3, 20000, 515, 32, "int4", "bias"),     # g = 32, ragged rows, K not a whole number of steps
+    (2, 40960, 2 * 777, 128, "int4", "swiglu"),
+    (4, 16384, 1001, 64, "int4", "residual"),
+    (4, 12288, 3003, 12288, "int8", None),   # per-channel scales
+    (8, 18944, 3584, 128, "int4", None),     # config 2 at M = 8: 8-row tiles, three K parts
+    (6, 8192, 1000, 64, "int4", "bias"),
+    (8, 3584, 2 * 1000, 3584, "int8", "swiglu"),
+    (7, 5024, 777, 32, "int4", "residual"),
+])
+def test_rows_kernel_k_parts(mn, gpu, M, K, N, g, qt, epi):
+    """Row-block kernel with K split into parts (activations longer than LDS):
+    the parts of a row block meet through the workspace, in K order."""
+    say(f"rows K parts M={M} K={K} N={N} g={g} {qt} {epi}")
+    if qt == "int4":
+        x, wp, s, z = O.make_int4_problem(M, K, N, g, seed=K + N)
+        Wd = O.dequant_int4(wp, s, z, K, g)
+    else:
+        x, wp, s, z, g = O.make_int8_problem(M, K, N, seed=N, g=g)
+        Wd = O.dequant_int8(wp, s, z, K, g)
+    acc = O.matmul_f32acc(x, Wd)
+    kw = {}
+    nout = N // 2 if epi == "swiglu" else N
+    if epi == "bias":
+        b = np.random.default_rng(N).standard_normal(N).astype(np.float16)
+        kw = dict(epilogue="bias", bias=dev(b, gpu))
+    elif epi == "swiglu":
+        kw = dict(epilogue="swiglu")
+    elif epi == "residual":
+        res = np.random.default_rng(3).standard_normal((M, N)).astype(np.float16)
+        kw = dict(epilogue="residual", residual=dev(res, gpu))
+    y, taken = run_dm(mn, gpu, x, wp, s, z, g, qt, "rows", **kw)
+    assert taken == "rows" and y.shape == (M, nout)
+    if epi == "swiglu":
+        check_swiglu(y, acc, "rows K parts swiglu")
+    elif epi == "bias":
+        check_close(y, acc + b.astype(np.float32), "rows K parts bias")
+    elif epi == "residual":
+        check_close(y, acc + res.astype(np.float32), "rows K parts residual")
+    else:
+        check_close(y, acc, "rows K parts")
+    # deterministic: the same bits on a second call
+    y2, _ = run_dm(mn, gpu, x, wp, s, z, g, qt, "rows", **kw)
+    np.testing.assert_array_equal(y2.view(np.uint16), y.view(np.uint16))
+
+
 @pytest.mark.parametrize("impl", [0, 1])
 @pytest.mark.parametrize("qt,g,epi", [("int4", 128, None), ("int4", 128, "bias"), ("int4", 128, "swiglu"),
                                       ("int4", 64, None), ("int4", 32, "bias_silu"), ("int4", 64, "swiglu"),
