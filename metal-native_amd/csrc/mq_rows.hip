@@ -68,11 +68,9 @@ struct RowsKArgs {
   uint32_t* cnt;  // KP > 1: arrivals per row block (zero between launches)
   int XS;         // LDS activation row stride (halves)
   int maxT;       // partial slots per wave
-  int szrows;     // weight rows whose scales are staged (R, or 2R for SwiGLU)
-  int szpad;      // zero entries after them
+  int snp;        // 16-byte scale pieces staged per region (one, or two for SwiGLU)
   uint32_t off_sz, off_scr, off_slot;  // LDS byte offsets
-  uint32_t a_bytes, sz_bytes, z_bytes;
-  uint64_t ppr_magic;  // ceil(2^32 / ppr): idx / ppr = (idx * magic) >> 32 for the staged index range
+  uint32_t sz_bytes, z_bytes;
   const _Float16* pre_delta; const _Float16* pre_weight; _Float16* pre_resid;  // fused pre-norm (PRE)
   float pre_eps;
 };
@@ -97,7 +95,7 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
   const int M = p.M, KS = min(p.KStot - ks0, p.KS);
 
   _Float16* xs = (_Float16*)smem;                     // [M][XS]
-  uint32_t* szl = (uint32_t*)(smem + p.off_sz);       // [szrows][G]: s | z << 16
+  uint32_t* szl = (uint32_t*)(smem + p.off_sz);       // [regions][8 snp]: s | z << 16
   float* scr = (float*)(smem + p.off_scr) + w * 256;  // per wave [16][16]
   float* slots = (float*)(smem + p.off_slot);         // [NW][maxT][M*RPW]
 
@@ -120,13 +118,6 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
     span = (uint32_t)(valid * p.ldw);
   }
   const rsrc_t wr = make_rsrc(p.W + (int64_t)row0 * p.ldw, span);
-  auto sz_row = [&](int t) -> int {  // this lane's local weight row of tile t
-    if (EPI == EPI_SWIGLU) {
-      const int c = t * HALF + (r % HALF);
-      return (r < HALF) ? c : p.R + c;
-    }
-    return t * RPW + r;
-  };
   auto row_off = [&](int t) -> uint32_t {  // byte offset of this lane's row of tile t, or kOob
     if (EPI == EPI_SWIGLU) {
       const int c = t * HALF + (r % HALF);
@@ -176,58 +167,69 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
   };
 
   // ---- staging loads, issued before the ring: the load counter completes
-  // in order, so staging data loaded after the ring would wait for it ----
-  const rsrc_t ar = make_rsrc(p.A, p.a_bytes);
-  const int ppr = p.KS * KSTEP / 8;   // whole units (the widest part): k past K is staged as zeros
+  // in order, so staging data loaded after the ring would wait for it.
+  // Every per-thread offset is a lane part computed once plus a uniform
+  // part: the staging runs on 3 waves per SIMD before the stream starts, so
+  // its VALU work is paid in full at the start of every launch ----
+  // activations: thread tid stages pieces c = tid + j*NT (j < epr) of each
+  // row i; one buffer resource per row, K*2 bytes long, so pieces past K
+  // read zeros
+  const int ppr = p.KS * KSTEP / 8;    // pieces per staged row (the widest part)
   const int kx0 = ks0 * KSTEP / 8;     // the part's first 16-byte piece of a row
-  const int npieces = M * ppr;
-  // exact batch sizes: every load instruction costs texture-unit time, even
-  // one whose lanes are all out of range
-  const int nxb = min(kXB, (npieces + NT - 1) / NT);
-  auto x_fetch = [&](int base, u4* v, int cnt) {
+  const int epr = (ppr + NT - 1) / NT;  // loads per row per thread
+  const int nxs = M * epr;              // staging slots per thread
+  const int nxb = min(kXB, nxs);
+  const uint32_t xvo = (uint32_t)(kx0 + tid) * 16u;                  // global offset, lane part
+  const uint32_t xlo = (uint32_t)(16 * tid + 16 * (tid >> 4));       // LDS offset of xswz(8 tid), bytes
+  auto x_row = [&](int i) { return make_rsrc(p.A + (int64_t)i * p.lda, (uint32_t)(p.K * 2)); };
+  auto x_fetch = [&](int s0, u4* v, int cnt) {
+    int i = s0 / epr, j = s0 - i * epr;   // uniform
 #pragma unroll
     for (int e = 0; e < kXB; ++e) {
       if (e < cnt) {
-        const int idx = base + tid + e * NT;
-        const int i = M == 1 ? 0 : (int)(((uint64_t)(uint32_t)idx * p.ppr_magic) >> 32), c = idx - i * ppr;
-        v[e] = bload16(ar, (idx < npieces && 8 * (kx0 + c) < p.K) ? (uint32_t)((i * p.lda + 8 * (kx0 + c)) * 2) : kOob);
+        v[e] = bload16(x_row(min(i, M - 1)), s0 + e < nxs ? xvo + (uint32_t)(j * NT * 16) : kOob);
+        if (++j == epr) { j = 0; ++i; }
       }
     }
   };
-  auto x_put = [&](int base, const u4* v, int cnt) {
+  auto x_put = [&](int s0, const u4* v, int cnt) {
+    int i = s0 / epr, j = s0 - i * epr;
 #pragma unroll
     for (int e = 0; e < kXB; ++e) {
-      const int idx = base + tid + e * NT;
-      if (e < cnt && idx < npieces) {
-        const int i = M == 1 ? 0 : (int)(((uint64_t)(uint32_t)idx * p.ppr_magic) >> 32), c = idx - i * ppr;
-        u4 vv = v[e];
-        if (FMT == FMT_INT4) vv = perm8_int4(vv);
-        *(u4*)(xs + i * p.XS + xswz(8 * c)) = vv;
+      if (e < cnt && s0 + e < nxs) {
+        if (tid + j * NT < ppr) {
+          u4 vv = v[e];
+          if (FMT == FMT_INT4) vv = perm8_int4(vv);
+          *(u4*)((unsigned char*)xs + i * p.XS * 2 + xlo + j * NT * 17) = vv;
+        }
+        if (++j == epr) { j = 0; ++i; }
       }
     }
   };
-  // scales/zeros of the workgroup's rows, [szrows][G] as s | z << 16.  The
-  // rows are one contiguous run of the [N][G] arrays (two for SwiGLU: gate
-  // and up rows), fetched as 16-byte pieces of 8 entries aligned to the
-  // array start; entries outside the run are dropped on the LDS write.
+  // scales/zeros, as s | z << 16 dwords: region 0 holds the 16-byte pieces
+  // of the [N][G] arrays that cover the entries of rows row0 .. row0+R-1
+  // plus the kstep/g entries that steps past K read (region 1, SwiGLU: the
+  // up rows F+row0 ..), copied whole from the piece boundary below the
+  // rows' first entry: entries outside the rows hold the neighbouring rows'
+  // finite scales or, past the arrays, zeros.
   const rsrc_t sr = make_rsrc(p.scales, p.sz_bytes);
   const rsrc_t zr = make_rsrc(p.zeros, p.z_bytes);
   const int G = p.G;
   const uint32_t sz_real = (uint32_t)p.N * (uint32_t)G * 2u;  // bytes of the scale array
-  const int run = valid * G;                                  // entries per run
-  const int eb0 = row0 * G;                                   // first entry of run 0
-  const int eb1 = (EPI == EPI_SWIGLU ? p.F + row0 : 0) * G;   // first entry of run 1
-  const int pb0 = eb0 >> 3, np0 = run > 0 ? ((eb0 + run + 7) >> 3) - pb0 : 0;
-  const int pb1 = eb1 >> 3, np1 = (EPI == EPI_SWIGLU && run > 0) ? ((eb1 + run + 7) >> 3) - pb1 : 0;
-  const int nps = FMT != FMT_F16 ? np0 + np1 : 0;
+  const int snp = p.snp;                                      // pieces per region
+  const int eb0 = row0 * G;                                   // first entry of region 0
+  const int eb1 = (EPI == EPI_SWIGLU ? p.F + row0 : 0) * G;   // first entry of region 1
+  const int pb0 = eb0 >> 3, pb1 = eb1 >> 3;
+  const int sb0 = eb0 & 7, sb1 = 8 * snp + (eb1 & 7);         // LDS entry of each region's first row
+  const int nps = FMT != FMT_F16 ? (EPI == EPI_SWIGLU ? 2 : 1) * snp : 0;
   const int nsb = min(kSB, (nps + NT - 1) / NT);
-  auto s_piece = [&](int idx) -> int { return idx < np0 ? pb0 + idx : pb1 + (idx - np0); };
   auto s_fetch = [&](int base, u4* sv, u4* zv, int cnt) {
 #pragma unroll
     for (int e = 0; e < kSB; ++e) {
       if (e < cnt) {
         const int idx = base + tid + e * NT;
-        const uint32_t off = idx < nps ? (uint32_t)s_piece(idx) * 16u : kOob;
+        const int gp = idx < snp ? pb0 + idx : pb1 - snp + idx;
+        const uint32_t off = idx < nps ? (uint32_t)gp * 16u : kOob;
         if (off == kOob || off + 16u <= sz_real) {
           sv[e] = bload16(sr, off);
           zv[e] = bload16(zr, off);
@@ -251,33 +253,14 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
     for (int e = 0; e < kSB; ++e) {
       const int idx = base + tid + e * NT;
       if (e < cnt && idx < nps) {
-        const bool second = idx >= np0;
-        const int eb = second ? eb1 : eb0;
-        const int d0 = second ? p.R * G : 0;   // LDS row block of run 1
-        const int ge = s_piece(idx) * 8;
-        const uint32_t sw[4] = {sv[e].x, sv[e].y, sv[e].z, sv[e].w};
-        const uint32_t zw[4] = {zv[e].x, zv[e].y, zv[e].z, zv[e].w};
-#pragma unroll
-        for (int h = 0; h < 8; ++h) {
-          const int le = ge + h - eb;
-          if (le >= 0 && le < run)
-            szl[d0 + le] = (h & 1) ? __builtin_amdgcn_perm(zw[h >> 1], sw[h >> 1], 0x07060302u)
-                                   : __builtin_amdgcn_perm(zw[h >> 1], sw[h >> 1], 0x05040100u);
-        }
+        const u4 a = sv[e], z = zv[e];
+        *(u4*)(szl + 8 * idx) = (u4){__builtin_amdgcn_perm(z.x, a.x, 0x05040100u), __builtin_amdgcn_perm(z.x, a.x, 0x07060302u),
+                                     __builtin_amdgcn_perm(z.y, a.y, 0x05040100u), __builtin_amdgcn_perm(z.y, a.y, 0x07060302u)};
+        *(u4*)(szl + 8 * idx + 4) = (u4){__builtin_amdgcn_perm(z.z, a.z, 0x05040100u), __builtin_amdgcn_perm(z.z, a.z, 0x07060302u),
+                                         __builtin_amdgcn_perm(z.w, a.w, 0x05040100u), __builtin_amdgcn_perm(z.w, a.w, 0x07060302u)};
       }
     }
   };
-  // the tail past the last staged row, read by steps past K, holds zeros
-  if (FMT != FMT_F16)
-    for (int i = tid; i < p.szpad; i += NT) szl[p.szrows * G + i] = 0u;
-  // rows past the valid ones (last workgroup) hold zero scales
-  if (FMT != FMT_F16 && valid < p.R) {
-    const int pad = (p.R - valid) * G, nrun = EPI == EPI_SWIGLU ? 2 : 1;
-    for (int i = tid; i < nrun * pad; i += NT) {
-      const int rr = i / pad;
-      szl[rr * p.R * G + run + (i - rr * pad)] = 0u;
-    }
-  }
 
   u4 raw[kD];
   {
@@ -291,8 +274,7 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
 #pragma unroll
       for (int e = 0; e < kXB; ++e) {
         if (e < nxb) {
-          const int idx = tid + e * NT;
-          const uint32_t off = (idx < npieces && 8 * idx < p.K) ? (uint32_t)(idx * 16) : kOob;
+          const uint32_t off = xvo + (uint32_t)(e * NT * 16);   // M = 1, one part: slot e is piece tid + e*NT
           dv[e] = bload16(dr, off);
           wv[e] = bload16(nr, off);
         }
@@ -329,7 +311,7 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
           for (int k = 0; k < 8; ++k) ss += (float)v[k] * (float)v[k];
           xv[e] = __builtin_bit_cast(u4, v);
           const int idx = tid + e * NT;
-          if (b == 0 && idx < npieces && 8 * idx < p.K) *(h8*)(p.pre_resid + 8 * idx) = v;
+          if (b == 0 && idx < ppr && 8 * idx < p.K) *(h8*)(p.pre_resid + 8 * idx) = v;
         }
       }
 #pragma unroll
@@ -359,10 +341,10 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
     for (int d = kPre; d < kD; ++d) raw[d] = wload();
   }
   // the rest (large M*K, many scale rows) after the ring
-  for (int base = kXB * NT; base < npieces; base += kXB * NT) {
+  for (int s0 = kXB; s0 < nxs; s0 += kXB) {
     u4 xv[kXB];
-    x_fetch(base, xv, kXB);
-    x_put(base, xv, kXB);
+    x_fetch(s0, xv, kXB);
+    x_put(s0, xv, kXB);
   }
   for (int base = kSB * NT; base < nps; base += kSB * NT) {
     u4 sv[kSB], zv[kSB];
@@ -385,7 +367,15 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
   // the next row's: any finite scale, the weights there meet zero activations)
   const int sadv = p.gshift >= 31 ? 0 : (KSTEP >> p.gshift);
   const int sl = p.gshift >= 31 ? 0 : (klane >> p.gshift);
-  int sa = sz_row(ct) * G + sl + (ks0 + cj) * sadv;
+  // LDS entry of this lane's row of tile t, group 0
+  auto sz_ent = [&](int t) -> int {
+    if (EPI == EPI_SWIGLU) {
+      const int c = t * HALF + (r % HALF);
+      return ((r < HALF) ? sb0 : sb1) + c * G;
+    }
+    return sb0 + (t * RPW + r) * G;
+  };
+  int sa = sz_ent(ct) + sl + (ks0 + cj) * sadv;
   const _Float16* xa = xs + xrow + xswz(cj * KSTEP + klane);
   static_assert(KSTEP % 128 == 0, "the LDS activation padding advances by a constant per unit");
   constexpr int XADV = KSTEP + (KSTEP >> 7) * 8;
@@ -458,7 +448,7 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
             cj = 0;
             ++ct;
             xa = xs + xrow + xswz(klane);
-            sa = sz_row(ct) * G + sl + ks0 * sadv;
+            sa = sz_ent(ct) + sl + ks0 * sadv;
           }
         }
       }
@@ -591,7 +581,6 @@ int gshift_of(const LinearArgs& a) {
   return -1;
 }
 int xswz_h(int k) { return k + ((k >> 7) << 3); }
-int szrows_of(const LinearArgs& a, int R) { return a.epi == EPI_SWIGLU ? 2 * R : R; }
 
 }  // namespace
 
@@ -645,12 +634,15 @@ RowsPlan rows_plan_k(const LinearArgs& a, int num_cus, int KP) {
   int XS = xswz_h(KS * kstep) + 8;
   XS = (XS + 127) / 128 * 128 + 64;  // rows of A fall 128 bytes apart in the LDS banks
   size_t off = al16((size_t)a.M * XS * 2);
-  const int szrows = a.epi == EPI_SWIGLU ? 2 * R : R;
   p.off_sz = (uint32_t)off;
-  // steps past K read up to kstep / g entries beyond a row's last group
+  // steps past K read up to kstep / g entries beyond a row's last group; a
+  // region starts up to 7 entries below its first row's
   const int szpad = quant && a.G != 1 ? kstep / a.g + 1 : 0;
   if (quant && a.G != 1 && kstep % a.g != 0) return p;   // the scale entry advances by whole groups per step
-  off += quant ? al16(((size_t)szrows * a.G + szpad) * 4) : 0;
+  const int64_t snp = quant ? (7 + (int64_t)R * a.G + szpad + 7) / 8 : 0;
+  const int nreg = a.epi == EPI_SWIGLU ? 2 : 1;
+  if (snp * nreg * 32 > (int64_t)kLds) return p;
+  off += (size_t)(snp * nreg * 32);
   p.off_scr = (uint32_t)off;
   off += (size_t)nw * 256 * 4;
   p.off_slot = (uint32_t)off;
@@ -662,19 +654,11 @@ RowsPlan rows_plan_k(const LinearArgs& a, int num_cus, int KP) {
     if (a.M != 1 || !quant || a.K % 8 || pieces > (int64_t)kXB * 64 * nw || !a.pre_weight || !a.pre_resid) return p;
     if (((uintptr_t)a.pre_weight | (uintptr_t)a.pre_resid | (uintptr_t)a.pre_delta) & 15) return p;
   }
-  {
-    // idx / d = (idx * ceil(2^32/d)) >> 32 is exact while idx * e < 2^32,
-    // e = ceil(2^32/d)*d - 2^32 < d; the staged index ranges are far below
-    const uint64_t ppr = (uint64_t)KS * kstep / 8;
-    const uint64_t n_x = (uint64_t)a.M * ppr, n_s = (uint64_t)szrows_of(a, R) * a.G;
-    if (n_x * ppr >= (1ull << 32) || n_s * (uint64_t)a.G >= (1ull << 32)) return p;
-  }
   p.rpw = rpw; p.nw = nw; p.nwg = nwg; p.R = R; p.TW = TW; p.KS = KS; p.XS = XS; p.maxT = maxT;
   p.KP = KP; p.nblk = nblk; p.KStot = KStot;
   p.ws_bytes = KP > 1 ? kCntBytesRows + (size_t)KP * nblk * a.M * R * (a.epi == EPI_SWIGLU ? 2 : 1) * 4 : 0;
   if (KP > 1 && (size_t)nblk * 4 > kCntBytesRows) return p;
-  p.szrows = szrows;
-  p.szpad = szpad;
+  p.snp = (int)snp;
   p.lds_bytes = off;
   p.ok = true;
   return p;
@@ -710,7 +694,7 @@ hipError_t rows_launch(const LinearArgs& a, const RowsPlan& pl, void* ws, hipStr
     k.cnt = (uint32_t*)ws;
     k.part = (float*)((char*)ws + kCntBytesRows);
   }
-  k.R = pl.R; k.TW = pl.TW; k.KS = pl.KS; k.XS = pl.XS; k.maxT = pl.maxT; k.szrows = pl.szrows; k.szpad = pl.szpad;
+  k.R = pl.R; k.TW = pl.TW; k.KS = pl.KS; k.XS = pl.XS; k.maxT = pl.maxT; k.snp = pl.snp;
   k.off_sz = pl.off_sz; k.off_scr = pl.off_scr; k.off_slot = pl.off_slot;
   if (a.prenorm) {
     k.pre_delta = (const _Float16*)a.pre_delta;
@@ -718,13 +702,8 @@ hipError_t rows_launch(const LinearArgs& a, const RowsPlan& pl, void* ws, hipStr
     k.pre_resid = (_Float16*)a.pre_resid;
     k.pre_eps = a.pre_eps;
   }
-  k.a_bytes = (uint32_t)(((int64_t)(a.M - 1) * a.lda + a.K) * 2);
   k.sz_bytes = a.fmt == FMT_F16 ? 0u : (uint32_t)(((int64_t)a.N * a.G * 2 + 3) & ~(int64_t)3);
   k.z_bytes = a.zeros ? k.sz_bytes : 0u;
-  {
-    const uint64_t ppr = (uint64_t)pl.KS * (4 * kpl_of(a.fmt) * (16 / pl.rpw)) / 8;
-    k.ppr_magic = ((1ull << 32) + ppr - 1) / ppr;
-  }
   switch (a.fmt) {
     case FMT_INT4: return launch1<FMT_INT4>(k, pl, a.epi, s);
     case FMT_INT8: return launch1<FMT_INT8>(k, pl, a.epi, s);
