@@ -289,7 +289,7 @@ __global__ __launch_bounds__(128) void attn_combine_kernel(const float* ws, _Flo
 // by recursive halving (LPR - 1 shuffles for LPR rows; lane q of a row group
 // ends with row q's score).  P.V: each lane weights its rows' V pieces and the
 // RPI row groups are summed by shuffles.  A wave keeps a running max / exp-sum
-// / P.V over its splits; wave 0 combines the waves' partials through LDS.
+// / P.V over its splits; the waves' partials meet through LDS, one thread per output dimension.
 // q and the new k are rotated and rounded to fp16 as rope_kv stores them; the
 // new token's k and v are taken from registers (its cache row is stale until
 // written) and written into the caches by the workgroup of the first query
@@ -426,20 +426,17 @@ __global__ __launch_bounds__(768) void attn_head_d_kernel(const _Float16* qkv, c
 #pragma unroll
     for (int e = 0; e < 8; ++e) wo[w][8 * q + e] = o_run[e];
   __syncthreads();
-  if (w == 0 && rg == 0) {
+  // the waves' partials meet in wave order, one thread per output dimension
+  if (tid < D) {
     float mm = -INFINITY;
     for (int ww = 0; ww < NW; ++ww) mm = fmaxf(mm, wm[ww]);
-    float ll = 0.f, o[8] = {};
+    float ll = 0.f, o = 0.f;
     for (int ww = 0; ww < NW; ++ww) {
       const float f = wm[ww] == -INFINITY ? 0.f : expf(wm[ww] - mm);
       ll += wl[ww] * f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] += wo[ww][8 * q + e] * f;
+      o += wo[ww][tid] * f;
     }
-    h8 r;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) r[e] = (_Float16)(o[e] / ll);
-    *(h8*)(out + h * D + 8 * q) = r;
+    out[h * D + tid] = (_Float16)(o / ll);
   }
 }
 
