@@ -281,7 +281,7 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
       }
     }
     if (FMT != FMT_F16) s_fetch(0, sv, zv, nsb);
-    // then a short head of the weight stream.  The staging data is waited
+    // Then a short head of the weight stream.  The staging data is waited
     // for before the rest: a wave blocks while the memory queues are full, so
     // a deep stream issued first would hold back the start of compute.
 #pragma unroll
