@@ -188,10 +188,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         dst[j].v[e] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(wr, vo + 16 * e, so, 0));
     }
   };
-  // scale|zero of tile t for each block (tiles past the range read entry 0)
+  // scale|zero of tile t for each block (tiles past the range read entry 0;
+  // a last K-tile half past K keeps the row's last group, not the next row's)
   auto read_sz = [&](int t, uint32_t (&dst)[NB]) {
     const int tc = t < kt1 ? t : kt0;
-    const int g = p.gshift >= 31 ? 0 : ((tc * KTK + 32 * h) >> p.gshift);
+    const int g = p.gshift >= 31 ? 0 : min((tc * KTK + 32 * h) >> p.gshift, p.G - 1);
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
       const int e = lrow(j) * p.G + g;

@@ -360,8 +360,10 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
   int ct = u0 / KS, cj = u0 - ct * KS;   // consume cursor (tile, step)
   const int ft = ct;                      // first tile of this wave
   // scale entry of the lane's row and group: the step advances it by a
-  // uniform KSTEP / g groups (k past K reads the zero-filled tail entries or
-  // the next row's: any finite scale, the weights there meet zero activations)
+  // uniform KSTEP / g groups.  In a row's last step, lanes whose k lies past
+  // K would reach the next row's entries: they keep their own row's last
+  // entry instead (the weights there meet zero activations, and a row's
+  // output must not depend on another row's scales, finite or not).
   const int sadv = p.gshift >= 31 ? 0 : (KSTEP >> p.gshift);
   const int sl = p.gshift >= 31 ? 0 : (klane >> p.gshift);
   // LDS entry of this lane's row of tile t, group 0
@@ -373,6 +375,10 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
     return sb0 + (t * RPW + r) * G;
   };
   int sa = sz_ent(ct) + sl + (ks0 + cj) * sadv;
+  auto clamp_last = [&]() {   // uniform condition: the row's last step
+    if (FMT != FMT_F16 && ks0 + cj == p.KStot - 1) sa = min(sa, sz_ent(ct) + G - 1);
+  };
+  clamp_last();
   const _Float16* xa = xs + xrow + xswz(cj * KSTEP + klane);
   static_assert(KSTEP % 128 == 0, "the LDS activation padding advances by a constant per unit");
   constexpr int XADV = KSTEP + (KSTEP >> 7) * 8;
@@ -448,6 +454,7 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
             sa = sz_ent(ct) + sl + ks0 * sadv;
           }
         }
+        clamp_last();
       }
       raw[d] = wload();
     }

@@ -737,3 +737,50 @@ def test_prefill_gemm_kernels(mn, gpu, impl, qt, g, epi, M, K, N):
         check_close(y, acc, f"gemm impl={impl}")
     else:
         check_epilogue(y, acc, epi, f"gemm impl={impl} {epi}", bias=b, residual=res)
+
+
+@pytest.mark.parametrize("path,M,K,N,g,qt,impl", [
+    ("rows", 1, 18944, 512, 128, "int4", 0),      # 18.5 steps of 1024: the last step's upper lanes are past K
+    ("rows", 4, 2016, 300, 32, "int4", 0),
+    ("rows", 2, 2016, 2 * 150, 32, "int4", 0),
+    ("rows", 1, 1216, 300, 64, "int8", 0),
+    ("decode", 1, 18944, 512, 128, "int4", 0),
+    ("decode", 8, 2016, 300, 32, "int4", 0),
+    ("decode", 12, 1216, 300, 64, "int8", 0),
+    ("tiled", 64, 3104, 256, 32, "int4", 0),       # K % 64 == 32: the last K-tile is half past K
+    ("tiled", 40, 2016, 200, 32, "int4", 0),
+    ("tiled", 64, 1216, 256, 64, "int8", 0),
+    ("tiled", 64, 3104, 256, 32, "int4", 1),       # the 16x16x32 tiled GEMM
+    ("tiled", 40, 1216, 256, 64, "int8", 1),
+    ("generic", 3, 1000, 100, 128, "int4", 0),
+])
+def test_weight_rows_do_not_see_other_rows_scales(mn, gpu, path, M, K, N, g, qt, impl):
+    """Output columns depend on their own weight row only, also where a
+    kernel's last step or K-tile reaches past K: non-finite scales and zeros
+    in some weight rows (as a corrupt checkpoint would hold) leave every other
+    column finite and within the bound, as in the reference, whose loops end at
+    K."""
+    say(f"row isolation {path} M={M} K={K} N={N} g={g} {qt}")
+    if qt == "int4":
+        x, wp, s, z = O.make_int4_problem(M, K, N, g, seed=K + N)
+    else:
+        x, wp, s, z, g = O.make_int8_problem(M, K, N, seed=K + N, g=g)
+    bad = [1, N // 2, N // 2 + 1, N - 1]
+    s = s.copy(); z = z.copy()
+    s[1] = np.float16(np.inf)
+    s[N // 2] = np.float16(np.nan)
+    z[N // 2 + 1] = np.float16(np.nan)
+    z[N - 1] = np.float16(-np.inf)
+    good = np.setdiff1d(np.arange(N), bad)
+    with np.errstate(invalid="ignore", over="ignore"):
+        Wd = O.dequant_int4(wp, s, z, K, g) if qt == "int4" else O.dequant_int8(wp, s, z, K, g)
+        acc = O.matmul_f32acc(x, Wd)
+    mn.set_option("gemm_impl", impl)
+    try:
+        y, taken = run_dm(mn, gpu, x, wp, s, z, g, qt, path)
+    finally:
+        mn.set_option("gemm_impl", 0)
+    expect_path(path, taken)
+    assert np.isfinite(y[:, good]).all(), (
+        f"{path}: columns {np.unique(np.nonzero(~np.isfinite(y[:, good]))[1])} of the good rows are not finite")
+    check_close(y[:, good], acc[:, good], f"row isolation {path}")
