@@ -17,7 +17,7 @@
 //  * Row tile: RPW weight rows x S = 16/RPW K shifts form the 16 columns of the
 //    B operand of v_mfma_f32_16x16x32_f16; one wave load reads RPW rows x 64*S
 //    contiguous bytes.  The A operand holds activation row i % RPW at K shift
-//    i / RPW (needs M <= RPW; RPW = 8 only for the quantized formats); the
+//    i / RPW (needs M <= RPW; RPW = 8 and 16 only for the quantized formats); the
 //    result for (activation i, weight row r) is sum_s D[s*RPW + i][s*RPW + r].
 //  * The workgroup's work is TW tiles x KS K-steps ("units", tile-major); wave
 //    w takes the contiguous units [w*U/NW, (w+1)*U/NW) and streams them
@@ -334,10 +334,10 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
     }
     x_put(0, xv, nxb);
     if (FMT != FMT_F16) s_put(0, sv, zv, nsb);
-#pragma unroll
-    for (int d = kPre; d < kD; ++d) raw[d] = wload();
   }
-  // the rest (large M*K, many scale rows) after the ring
+  // the rest (large M*K, many scale rows), then the rest of the ring: loads
+  // complete in order, so staging loads issued behind the ring would wait
+  // for its weights
   for (int s0 = kXB; s0 < nxs; s0 += kXB) {
     u4 xv[kXB];
     x_fetch(s0, xv, kXB);
@@ -348,6 +348,8 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
     s_fetch(base, sv, zv, kSB);
     s_put(base, sv, zv, kSB);
   }
+#pragma unroll
+  for (int d = kPre; d < kD; ++d) raw[d] = wload();
   // LDS barrier that leaves the weight loads in flight
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
@@ -380,7 +382,10 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
   };
   clamp_last();
   const _Float16* xa = xs + xrow + xswz(cj * KSTEP + klane);
-  static_assert(KSTEP % 128 == 0, "the LDS activation padding advances by a constant per unit");
+  // the LDS activation padding (8 halves per 128) advances by a constant per
+  // unit when a unit spans whole 128-k blocks; otherwise (16-row int8 tiles,
+  // 64 k per unit) the fragment address is recomputed per unit
+  constexpr bool XCONST = KSTEP % 128 == 0;
   constexpr int XADV = KSTEP + (KSTEP >> 7) * 8;
   f4 acc = (f4){0.f, 0.f, 0.f, 0.f};
 
@@ -389,12 +394,12 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) scr[(4 * gi + e) * 16 + nl] = acc[e];
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    if (lane < M * RPW) {
-      const int i = lane / RPW, rr = lane - i * RPW;
+    for (int idx = lane; idx < M * RPW; idx += 64) {   // one pass but for 16-row tiles
+      const int i = idx / RPW, rr = idx - i * RPW;
       float v = 0.f;
 #pragma unroll
       for (int s = 0; s < S; ++s) v += scr[(s * RPW + i) * 16 + s * RPW + rr];
-      slots[(w * p.maxT + (ct - ft)) * (M * RPW) + lane] = v;
+      slots[(w * p.maxT + (ct - ft)) * (M * RPW) + idx] = v;
     }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     acc = (f4){0.f, 0.f, 0.f, 0.f};
@@ -442,7 +447,7 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
         if (base + d == q2) __builtin_amdgcn_s_setprio(1);
         if (base + d == q3) __builtin_amdgcn_s_setprio(0);
         step(raw[d]);
-        xa += XADV;
+        if constexpr (XCONST) xa += XADV;
         sa += sadv;
         const bool last = base + d == nu - 1;
         if (++cj == KS || last) {
@@ -454,6 +459,7 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
             sa = sz_ent(ct) + sl + ks0 * sadv;
           }
         }
+        if constexpr (!XCONST) xa = xs + xrow + xswz(cj * KSTEP + klane);
         clamp_last();
       }
       raw[d] = wload();
@@ -566,6 +572,9 @@ hipError_t launch2(const RowsKArgs& k, const RowsPlan& pl, hipStream_t s) {
     case 8:   // 8-row tiles: 2 K shifts, quantized formats only (an fp16 step would be 64 k)
       if constexpr (FMT != FMT_F16) return launch3<FMT, EPI, 8>(k, pl, s);
       return hipErrorInvalidValue;
+    case 16:   // 16-row tiles, no K shift: M = 9..16, quantized formats only
+      if constexpr (FMT != FMT_F16) return launch3<FMT, EPI, 16>(k, pl, s);
+      return hipErrorInvalidValue;
     default: return hipErrorInvalidValue;
   }
 }
@@ -594,7 +603,7 @@ RowsPlan rows_plan_k(const LinearArgs& a, int num_cus, int KP) {
   RowsPlan p{};
   p.ok = false;
   const int kpl = kpl_of(a.fmt);
-  if (a.M < 1 || a.M > (a.fmt == FMT_F16 ? 4 : 8)) return p;
+  if (a.M < 1 || a.M > (a.fmt == FMT_F16 ? 4 : 16)) return p;
   if (a.K % kpl != 0 || (a.K & 7)) return p;
   if (a.fmt != FMT_F16 && a.G != 1 && (gshift_of(a) < 0 || a.g < kpl)) return p;
   if (((uintptr_t)a.W & 15) || (a.ldw & 15)) return p;
@@ -609,8 +618,8 @@ RowsPlan rows_plan_k(const LinearArgs& a, int num_cus, int KP) {
   // workgroup rounded up to whole tiles, times K rounded up to whole steps
   int rpw = 4;
   double best_work = 1e300;
-  for (int cand = 1; cand <= (a.fmt == FMT_F16 ? 4 : 8); cand <<= 1) {
-    if (cand < a.M || (a.epi == EPI_SWIGLU && cand < 2)) continue;
+  for (int cand = 1; cand <= (a.fmt == FMT_F16 ? 4 : 16); cand <<= 1) {
+    if (cand < a.M || (a.epi == EPI_SWIGLU && cand < 2) || (cand == 16 && a.M <= 8)) continue;
     const int ks = 4 * kpl * (16 / cand);
     const int gr = a.epi == EPI_SWIGLU ? cand / 2 : cand;
     const int rr = ((nrows + num_cus - 1) / num_cus + gr - 1) / gr * gr;
@@ -636,7 +645,10 @@ RowsPlan rows_plan_k(const LinearArgs& a, int num_cus, int KP) {
   const int maxT = per / KS + 2;
   if ((int64_t)(a.epi == EPI_SWIGLU ? a.F + R : R) * a.ldw >= lim) return p;
   int XS = xswz_h(KS * kstep) + 8;
-  XS = (XS + 127) / 128 * 128 + 64;  // rows of A fall 128 bytes apart in the LDS banks
+  // the LDS row stride of A (mod 256 bytes): 128 bytes for tiles with K
+  // shifts; 16 bytes for 16-row tiles, whose 16 fragment rows (one per lane
+  // of a 16-lane group) then fall in different banks
+  XS = (XS + 127) / 128 * 128 + (rpw == 16 ? 8 : 64);
   size_t off = al16((size_t)a.M * XS * 2);
   p.off_sz = (uint32_t)off;
   // steps past K read up to kstep / g entries beyond a row's last group; a

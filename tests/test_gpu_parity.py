@@ -657,10 +657,17 @@ def test_rows_kernel_ragged_runs(mn, gpu, M, K, N, g, qt, epi):
     (6, 8192, 1000, 64, "int4", "bias"),
     (8, 3584, 2 * 1000, 3584, "int8", "swiglu"),
     (7, 5024, 777, 32, "int4", "residual"),
+    (16, 3584, 2 * 1000, 3584, "int8", "swiglu"),   # 16-row tiles (M = 9..16), config-4 class
+    (12, 4096, 1000, 128, "int4", None),
+    (9, 2048, 515, 64, "int4", "bias"),
+    (10, 1200, 300, 1200, "int8", None),     # int8 16-row units of 64 k: the last one half past K
+    (13, 1216, 300, 64, "int8", "residual"),
+    (16, 8192, 1024, 128, "int4", None),     # 16 rows over K = 8192: K parts
 ])
 def test_rows_kernel_k_parts(mn, gpu, M, K, N, g, qt, epi):
     """Row-block kernel with K split into parts (activations longer than LDS):
-    the parts of a row block meet through the workspace, in K order."""
+    the parts of a row block meet through the workspace, in K order; and its
+    16-row tiles for M = 9..16."""
     say(f"rows K parts M={M} K={K} N={N} g={g} {qt} {epi}")
     if qt == "int4":
         x, wp, s, z = O.make_int4_problem(M, K, N, g, seed=K + N)
