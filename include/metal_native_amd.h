@@ -76,8 +76,9 @@ enum mq_epilogue {
  * bias is read only by the bias epilogues, residual (fp16 [M, N], row stride
  * ldr >= N) only by MQ_EPILOGUE_RESIDUAL; the residual may be the output
  * itself when ldr == ldc (each element is read and then written by one
- * thread).  The decode GEMV (M <= 16) splits K across workgroups; its
- * partial sums and counters live in a library workspace kept per (device,
+ * thread).  The decode kernels (M <= 16) that split K across workgroups
+ * (the split-K GEMV, and the row-block GEMV when the activations exceed LDS)
+ * keep their partial sums and counters in a library workspace per (device,
  * stream), allocated by the first call on that stream that needs it (so that
  * call must not be inside stream capture).  Calls on one stream are ordered
  * and share it. */
