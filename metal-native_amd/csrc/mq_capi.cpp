@@ -125,13 +125,12 @@ int choose_path(const mq::LinearArgs& a) {
   if (forced == PATH_DECODE && decode_ok(a)) return PATH_DECODE;
   if (forced == PATH_TILED && prefill_ok(a)) return PATH_TILED;
   if (forced == PATH_GENERIC) return PATH_GENERIC;
-  // automatic choice: the row-block kernel up to M = 4 (its 8-row tiles for
-  // M = 5..8 measured slower than the split-K GEMV at config 2: 20.3 vs
-  // 18.2 us), and its 16-row tiles for M = 9..16 where the activations fit
-  // in LDS whole (config 4 at M = 16: 39.6 vs 45.4 us); forced, it takes
-  // M <= 16
+  // automatic choice: the row-block kernel up to M = 4; for M = 5..16 only
+  // where the activations fit in LDS whole (its K parts measured slower than
+  // the split-K GEMV at config 2, M = 8: 20.3 vs 18.2 us; whole, it is
+  // faster: config 4 at M = 8, 29.5 vs 40.3 us, at M = 16, 39.6 vs 45.4 us)
   if (a.M <= 4 && rows_ok(a)) return PATH_ROWS;
-  if (a.M >= 9 && a.M <= 16) {
+  if (a.M <= 16) {
     const mq::RowsPlan pl = mq::rows_plan(a, num_cus_current());
     if (pl.ok && pl.KP == 1) return PATH_ROWS;
   }
