@@ -210,8 +210,9 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
   // of the [N][G] arrays that cover the entries of rows row0 .. row0+R-1
   // plus the kstep/g entries that steps past K read (region 1, SwiGLU: the
   // up rows F+row0 ..), copied whole from the piece boundary below the
-  // rows' first entry: entries outside the rows hold the neighbouring rows'
-  // finite scales or, past the arrays, zeros.
+  // rows' first entry.  Entries outside the rows (the neighbouring rows',
+  // or zeros past the arrays) feed only rows past N, whose outputs are not
+  // stored: lanes past K keep their own row's last entry (below).
   const rsrc_t sr = make_rsrc(p.scales, p.sz_bytes);
   const rsrc_t zr = make_rsrc(p.zeros, p.z_bytes);
   const int G = p.G;
