@@ -90,7 +90,7 @@ hipError_t gemv_scratch(hipStream_t s, void** ptr);
 struct RowsPlan {
   int rpw, nw, nwg, R, TW, KS, XS, maxT, snp;
   int KP, nblk, KStot;
-  uint32_t off_sz, off_scr, off_slot;
+  uint32_t off_sz, off_scr, off_slot, off_wft;
   size_t lds_bytes, ws_bytes;
   bool ok;
 };

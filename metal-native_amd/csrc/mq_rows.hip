@@ -46,6 +46,7 @@ namespace {
 
 constexpr int kD = 4;        // ring depth (units in flight per wave)
 constexpr int kNW = 12;      // wavefronts per workgroup
+static_assert(kNW % 4 == 0, "the slot sums read the first-tile table in groups of four");
 constexpr int kPre = 2;      // ring slots issued before the staging data is waited for
 constexpr int kXB = 8;           // activation pieces per thread per staging batch
 constexpr int kSB = 2;           // scale/zero pieces per thread per staging batch
@@ -69,7 +70,7 @@ struct RowsKArgs {
   int XS;         // LDS activation row stride (halves)
   int maxT;       // partial slots per wave
   int snp;        // 16-byte scale pieces staged per region (one, or two for SwiGLU)
-  uint32_t off_sz, off_scr, off_slot;  // LDS byte offsets
+  uint32_t off_sz, off_scr, off_slot, off_wft;  // LDS byte offsets
   uint32_t sz_bytes, z_bytes;
   const _Float16* pre_delta; const _Float16* pre_weight; _Float16* pre_resid;  // fused pre-norm (PRE)
   float pre_eps;
@@ -98,6 +99,7 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
   uint32_t* szl = (uint32_t*)(smem + p.off_sz);       // [regions][8 snp]: s | z << 16
   float* scr = (float*)(smem + p.off_scr) + w * 256;  // per wave [16][16]
   float* slots = (float*)(smem + p.off_slot);         // [NW][maxT][M*RPW]
+  int* wft = (int*)(smem + p.off_wft);                // [NW] first tile of each wave's unit range
 
   const int nl = lane & 15, gi = lane >> 4;
   const int r = nl % RPW, sh = nl / RPW;              // weight row in tile, K shift
@@ -362,6 +364,7 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
 
   int ct = u0 / KS, cj = u0 - ct * KS;   // consume cursor (tile, step)
   const int ft = ct;                      // first tile of this wave
+  if (lane == 0) wft[w] = ft;   // read by the slot sums after the final barrier
   // scale entry of the lane's row and group: the step advances it by a
   // uniform KSTEP / g groups.  In a row's last step, lanes whose k lies past
   // K would reach the next row's entries: they keep their own row's last
@@ -471,12 +474,30 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
   // ---- sum the slots per output, epilogue ----
   const int MR = M * RPW;
   auto tile_sum = [&](int t, int i, int rr) -> float {
-    float v = 0.f;
+    // Every wave's first tile and slot entry are read unconditionally (the
+    // index of a wave that did not touch the tile is masked to entry 0, its
+    // value to +0), so the reads are in flight together instead of one LDS
+    // round trip per wave; the sum keeps wave order, and adding +0 to a sum
+    // that starts at +0 leaves it bit-identical.
     const int ub = t * KS, ue = ub + KS;
+    int fw[NW];
+#pragma unroll
+    for (int ww = 0; ww < NW; ww += 4) {
+      const int4 f4 = *(const int4*)(wft + ww);
+      fw[ww] = f4.x; fw[ww + 1] = f4.y; fw[ww + 2] = f4.z; fw[ww + 3] = f4.w;
+    }
+    float sv[NW];
+    bool use[NW];
+#pragma unroll
     for (int ww = 0; ww < NW; ++ww) {
       const int a0 = (ww * U) / NW, a1 = ((ww + 1) * U) / NW;
-      if (a0 < ue && a1 > ub && a1 > a0) v += slots[(ww * p.maxT + (t - a0 / KS)) * MR + i * RPW + rr];
+      use[ww] = a0 < ue && a1 > ub && a1 > a0;
+      const int idx = ((ww * p.maxT + (t - fw[ww])) * MR + i * RPW + rr) & -(int)use[ww];
+      sv[ww] = slots[idx];
     }
+    float v = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < NW; ++ww) v += use[ww] ? sv[ww] : 0.f;
     return v;
   };
   if (p.KP > 1) {
@@ -664,6 +685,8 @@ RowsPlan rows_plan_k(const LinearArgs& a, int num_cus, int KP) {
   off += (size_t)nw * 256 * 4;
   p.off_slot = (uint32_t)off;
   off += al16((size_t)nw * maxT * a.M * rpw * 4);
+  p.off_wft = (uint32_t)off;
+  off += al16((size_t)nw * 4);
   if (off > kLds) return p;
   if ((int64_t)U * nw >= ((int64_t)1 << 31)) return p;  // unit ranges in 32-bit arithmetic
   if (a.prenorm) {  // one staging batch, whole 16-byte pieces, M = 1
@@ -712,7 +735,7 @@ hipError_t rows_launch(const LinearArgs& a, const RowsPlan& pl, void* ws, hipStr
     k.part = (float*)((char*)ws + kCntBytesRows);
   }
   k.R = pl.R; k.TW = pl.TW; k.KS = pl.KS; k.XS = pl.XS; k.maxT = pl.maxT; k.snp = pl.snp;
-  k.off_sz = pl.off_sz; k.off_scr = pl.off_scr; k.off_slot = pl.off_slot;
+  k.off_sz = pl.off_sz; k.off_scr = pl.off_scr; k.off_slot = pl.off_slot; k.off_wft = pl.off_wft;
   if (a.prenorm) {
     k.pre_delta = (const _Float16*)a.pre_delta;
     k.pre_weight = (const _Float16*)a.pre_weight;
