@@ -791,3 +791,55 @@ def test_weight_rows_do_not_see_other_rows_scales(mn, gpu, path, M, K, N, g, qt,
     assert np.isfinite(y[:, good]).all(), (
         f"{path}: columns {np.unique(np.nonzero(~np.isfinite(y[:, good]))[1])} of the good rows are not finite")
     check_close(y[:, good], acc[:, good], f"row isolation {path}")
+
+
+# ---------------------------------------------------------------------------
+# in-kernel dequant bit-exact on every path: one-hot activations
+# ---------------------------------------------------------------------------
+
+# finite weights only (a zero activation times an infinite weight is NaN):
+# subnormal, smallest normal, ~0.1, 1, ~256, ~4094 and 8188 (the largest
+# scale whose -8s is finite) scales, negative ones, and zeros of every sign
+ONEHOT_SCALES = np.array([0x0001, 0x03FF, 0x0400, 0x2E66, 0x3C00, 0x5BFF, 0x6BFF, 0x6FFF, 0xAE66, 0x8001,
+                          0xEFFF, 0x0000], dtype=np.uint16)
+ONEHOT_ZEROS = np.array([0x0000, 0x8000, 0x0001, 0x3C00, 0xBC00, 0x2E66, 0x4A00], dtype=np.uint16)
+
+
+@pytest.mark.parametrize("qt", ["int4", "int8"])
+@pytest.mark.parametrize("path,impl,M", [("rows", 0, 8), ("decode", 0, 8), ("generic", 0, 8), ("tiled", 0, 64),
+                                         ("tiled", 1, 64)])
+def test_one_hot_selects_dequantized_weights(mn, gpu, qt, path, impl, M):
+    """One-hot activation rows make every output the fp32 sum of one product
+    w * 1 and zeros, i.e. the dequantized weight itself: each kernel's
+    in-register dequant must equal the oracle's two-rounding weights exactly
+    (up to the sign of zero), over special scales and zeros."""
+    say(f"one-hot {qt} {path} impl={impl} M={M}")
+    rng = np.random.default_rng(11)
+    N, K, g = 256, 512, 64
+    G = K // g
+    s = ONEHOT_SCALES[rng.integers(0, len(ONEHOT_SCALES), (N, G))].view(np.float16)
+    z = ONEHOT_ZEROS[rng.integers(0, len(ONEHOT_ZEROS), (N, G))].view(np.float16)
+    if qt == "int4":
+        wp = rng.integers(0, 256, (N, K // 2), dtype=np.uint8)
+        want = O.dequant_int4(wp, s, z, K, g)
+    else:
+        s = np.minimum(np.abs(s.astype(np.float32)), 255.0).astype(np.float16) * np.sign(s.astype(np.float32)).astype(np.float16)
+        wp = rng.integers(-127, 128, (N, K), dtype=np.int16).astype(np.int8)
+        want = O.dequant_int8(wp, s, z, K, g)
+    assert np.isfinite(want).all()
+    ks_all = rng.permutation(K)
+    mn.set_option("gemm_impl", impl)
+    try:
+        for rep in range(2):
+            ks = ks_all[rep * M:(rep + 1) * M]
+            x = np.zeros((M, K), dtype=np.float16)
+            x[np.arange(M), ks] = 1.0
+            y, taken = run_dm(mn, gpu, x, wp, s, z, g, qt, path)
+            expect_path(path, taken)
+            ref = want[:, ks].T                              # [M, N]
+            assert np.isfinite(y).all(), f"{path}: non-finite outputs"
+            bad = y != ref                                   # -0 == +0
+            assert not bad.any(), (f"{qt} {path} impl={impl}: {bad.sum()} outputs differ from the dequantized "
+                                   f"weights, e.g. {y[bad][:4]} vs {ref[bad][:4]}")
+    finally:
+        mn.set_option("gemm_impl", 0)
