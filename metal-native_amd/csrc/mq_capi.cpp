@@ -35,16 +35,16 @@ int hip_fail(hipError_t e, const char* what) {
 }
 
 int num_cus_current() {
-  static int cache[64] = {0};
+  static std::atomic<int> cache[64] = {};   // per device; threads may race to fill in the same value
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cache[dev] == 0) {
-    int n = 0;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
       n = 256;
-    cache[dev] = n;
+    cache[dev].store(n, std::memory_order_relaxed);
   }
-  return cache[dev];
+  return n;
 }
 
 // Path ids (mq_last_path / force_path); 1 and 5 are retired ids of earlier
@@ -72,7 +72,7 @@ bool decode_ok(const mq::LinearArgs& a) {
 }
 
 // Split-K workspace, one per (device, stream): counters must start at zero and
-// every launch leaves them at zero, so one hipMemset at allocation suffices.
+// every launch leaves them at zero, so one fill at allocation suffices.
 // Calls on one stream are ordered, so they may share it.
 struct Workspace {
   void* ptr = nullptr;
@@ -104,7 +104,10 @@ hipError_t workspace_for(hipStream_t s, size_t need, void** out) {
     void* p = nullptr;
     e = hipMalloc(&p, nb);
     if (e != hipSuccess) return e;
-    e = hipMemset(p, 0, nb);
+    // zeroed on the stream that uses it, so the first kernel on that stream
+    // is ordered after the fill whatever the stream's flags (never inside a
+    // capture: refused above)
+    e = hipMemsetAsync(p, 0, nb, s);
     if (e != hipSuccess) { (void)hipFree(p); return e; }
     w.ptr = p;
     w.bytes = nb;
