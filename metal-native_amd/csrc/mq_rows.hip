@@ -637,7 +637,11 @@ RowsPlan rows_plan_k(const LinearArgs& a, int num_cus, int KP) {
   const bool quant = a.fmt != FMT_F16;
   const int nrows = a.epi == EPI_SWIGLU ? a.F : a.N;
   // the tile width (>= M rows) with the least padded work per CU: rows per
-  // workgroup rounded up to whole tiles, times K rounded up to whole steps
+  // workgroup rounded up to whole tiles, times K rounded up to whole steps,
+  // for M = 1 less 3 % per doubling of the tile width (measured, int4,
+  // K = 3584: 4 or 8 rows per tile 3-5 % faster than 1 or 2 at equal padded
+  // work; K = 18944: 2 and 8 equal), otherwise 1 % more per row of width
+  // (config 2 at M = 4: 4-row tiles 4 % faster than 8-row ones)
   int rpw = 4;
   double best_work = 1e300;
   for (int cand = 1; cand <= (a.fmt == FMT_F16 ? 4 : 16); cand <<= 1) {
@@ -645,7 +649,8 @@ RowsPlan rows_plan_k(const LinearArgs& a, int num_cus, int KP) {
     const int ks = 4 * kpl * (16 / cand);
     const int gr = a.epi == EPI_SWIGLU ? cand / 2 : cand;
     const int rr = ((nrows + num_cus - 1) / num_cus + gr - 1) / gr * gr;
-    const double work = (double)rr * ((a.K + ks - 1) / ks * ks) * (1.0 + 0.01 * cand);
+    const double pref = a.M == 1 ? 1.0 - 0.03 * __builtin_ctz(cand) : 1.0 + 0.01 * cand;
+    const double work = (double)rr * ((a.K + ks - 1) / ks * ks) * pref;
     if (work < best_work) { best_work = work; rpw = cand; }
   }
   const int S = 16 / rpw;
