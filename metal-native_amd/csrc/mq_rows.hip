@@ -45,8 +45,12 @@ namespace mq {
 namespace {
 
 constexpr int kD = 4;        // ring depth (units in flight per wave)
-constexpr int kNW = 12;      // wavefronts per workgroup
-static_assert(kNW % 4 == 0, "the slot sums read the first-tile table in groups of four");
+// wavefronts per workgroup: 12, or 8 when the workgroup streams at most
+// kSmallBytes of weights (measured at M = 1: 8 waves 4-8 % faster at 2-8 MB
+// in total, 3-4 % slower at 34 MB and more)
+constexpr int kNWBig = 12, kNWSmall = 8;
+constexpr int64_t kSmallBytes = 64 * 1024;
+static_assert(kNWBig % 4 == 0 && kNWSmall % 4 == 0, "the slot sums read the first-tile table in groups of four");
 constexpr int kPre = 2;      // ring slots issued before the staging data is waited for
 constexpr int kXB = 8;           // activation pieces per thread per staging batch
 constexpr int kSB = 2;           // scale/zero pieces per thread per staging batch
@@ -76,8 +80,8 @@ struct RowsKArgs {
   float pre_eps;
 };
 
-template <int FMT, int EPI, int RPW, bool PRE>
-__global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
+template <int FMT, int EPI, int RPW, bool PRE, int NW>
+__global__ __launch_bounds__(64 * NW) void rows_kernel(RowsKArgs p) {
   constexpr int S = 16 / RPW;
   constexpr int KPL = FmtTraits<FMT>::KPL;       // k per 16-byte piece
   constexpr int KSTEP = 4 * KPL * S;             // k per row per unit
@@ -86,8 +90,7 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
   constexpr int BPK2 = (FMT == FMT_INT4) ? 1 : (FMT == FMT_INT8 ? 2 : 4);  // 2 x bytes per k
   extern __shared__ __align__(16) unsigned char smem[];
 
-  constexpr int NW = kNW;
-  constexpr int NT = 64 * kNW;
+  constexpr int NT = 64 * NW;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   // K part kpi of row block b: steps [ks0, ks0 + KS) of the row
@@ -568,13 +571,20 @@ __global__ __launch_bounds__(64 * kNW) void rows_kernel(RowsKArgs p) {
   }
 }
 
-template <int FMT, int EPI, int RPW, bool PRE>
-hipError_t launch4(const RowsKArgs& k, const RowsPlan& pl, hipStream_t s) {
-  auto fn = rows_kernel<FMT, EPI, RPW, PRE>;
+template <int FMT, int EPI, int RPW, bool PRE, int NW>
+hipError_t launch5(const RowsKArgs& k, const RowsPlan& pl, hipStream_t s) {
+  auto fn = rows_kernel<FMT, EPI, RPW, PRE, NW>;
   hipError_t e = allow_dynamic_lds((const void*)fn, (int)kLds);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(fn, dim3(pl.nwg), dim3(64 * kNW), pl.lds_bytes, s, k);
+  hipLaunchKernelGGL(fn, dim3(pl.nwg), dim3(64 * NW), pl.lds_bytes, s, k);
   return hipGetLastError();
+}
+
+template <int FMT, int EPI, int RPW, bool PRE>
+hipError_t launch4(const RowsKArgs& k, const RowsPlan& pl, hipStream_t s) {
+  if (pl.nw == kNWSmall) return launch5<FMT, EPI, RPW, PRE, kNWSmall>(k, pl, s);
+  if (pl.nw == kNWBig) return launch5<FMT, EPI, RPW, PRE, kNWBig>(k, pl, s);
+  return hipErrorInvalidValue;
 }
 
 template <int FMT, int EPI, int RPW>
@@ -667,7 +677,8 @@ RowsPlan rows_plan_k(const LinearArgs& a, int num_cus, int KP) {
   const int KS = (KStot + KP - 1) / KP;   // steps per part
   if (KP > 1 && (int64_t)KS * (KP - 1) >= KStot) return p;   // every part has steps
   const int U = TW * KS;
-  const int nw = kNW;
+  const int64_t wbytes = (int64_t)(a.epi == EPI_SWIGLU ? 2 * R : R) * a.ldw / KP;   // weight bytes per workgroup
+  const int nw = wbytes <= kSmallBytes ? kNWSmall : kNWBig;
   const int per = (U + nw - 1) / nw;
   const int maxT = per / KS + 2;
   if ((int64_t)(a.epi == EPI_SWIGLU ? a.F + R : R) * a.ldw >= lim) return p;
