@@ -7,7 +7,7 @@
 // fp16 B [N, K]), computing every row of A.
 //
 // Structure (one launch; no workgroup waits for another):
-//  * One workgroup of NW wavefronts per CU.  Workgroup b owns R consecutive
+//  * One workgroup of NW (12, or 8 for small problems) wavefronts per CU.  Workgroup b owns R consecutive
 //    output rows (SwiGLU: R output columns = R gate + R up weight rows) over
 //    the whole of K, so every CU streams the same number of weight bytes.
 //    When the activations of all of K do not fit in LDS (M = 4 at K = 18944),
