@@ -76,9 +76,9 @@ enum mq_epilogue {
  * bias is read only by the bias epilogues, residual (fp16 [M, N], row stride
  * ldr >= N) only by MQ_EPILOGUE_RESIDUAL; the residual may be the output
  * itself when ldr == ldc (each element is read and then written by one
- * thread).  The decode kernels (M <= 16) that split K across workgroups
- * (the split-K GEMV, and the row-block GEMV when the activations exceed LDS)
- * keep their partial sums and counters in a library workspace per (device,
+ * thread).  The kernels that split K across workgroups (the split-K GEMV,
+ * the row-block GEMV when the activations exceed LDS, and the prefill GEMM
+ * where its output tiles would leave most CUs idle) keep their partial sums and counters in a library workspace per (device,
  * stream), allocated by the first call on that stream that needs it (so that
  * call must not be inside stream capture).  Calls on one stream are ordered
  * and share it. */
@@ -94,7 +94,8 @@ MQ_API int mq_dequant_matmul(const void* activations, int64_t lda, const void* w
  * contract and kernels as mq_dequant_matmul; where the split-K decode GEMV
  * runs, its counters and partial sums live in a fixed 8 MiB device array of
  * the library (one per GPU, held until the process ends) instead of the
- * per-stream workspace.  A shape whose split-K partials need more than that
+ * per-stream workspace; the prefill GEMM keeps one workgroup per output tile
+ * (no K split) here.  A shape whose split-K partials need more than that
  * returns MQ_INVALID_ARGUMENT with the sizes in mq_last_error().  The first
  * call on a device clears the array's counters with a kernel on the given
  * stream; every call leaves them zero.  Calls that overlap on one GPU share
@@ -225,7 +226,9 @@ MQ_API int mq_argmax_embed_f16(const void* logits, int64_t vocab, const void* em
  * "gemv_tiles_per_wg" (row tiles per workgroup: 1, 2 or 4, 0 automatic),
  * "gemm_impl" (prefill GEMM kernel: 0 the register-operand 32x32x16 kernel
  * where it takes the shape, 1 always the 16x16x32 tiled kernel; both compute
- * the same contract).  A forced path that cannot take the shape falls back
+ * the same contract), "gemm_split" (1, the default: the 32x32x16 kernel splits
+ * K over several workgroups per output tile where its tiles would leave CUs
+ * idle, summing the parts in a fixed order; 0: one workgroup per tile).  A forced path that cannot take the shape falls back
  * to the automatic choice.  Returns MQ_INVALID_ARGUMENT for an unknown key or
  * value. */
 MQ_API int mq_set_option(const char* key, int64_t value);
@@ -233,7 +236,8 @@ MQ_API int mq_set_option(const char* key, int64_t value);
 /* Kernel the last successful mq_dequant_matmul / mq_vecmat_f16 /
  * mq_vecmat_f32 call on this thread launched: 2 16x16x32 tiled GEMM, 3
  * generic, 4 vecmat [K,N], 6 split-K decode GEMV, 7 row-block decode GEMV, 8
- * 32x32x16 prefill GEMM, 9 fp32 vecmat. */
+ * 32x32x16 prefill GEMM, 9 fp32 vecmat, 10 32x32x16 prefill GEMM with K split
+ * over workgroups. */
 MQ_API int mq_last_path(void);
 
 MQ_API const char* mq_last_error(void);

@@ -50,15 +50,18 @@ int num_cus_current() {
 // Path ids (mq_last_path / force_path); 1 and 5 are retired ids of earlier
 // decode kernels and are not reused.
 // PATH_TILED selects the prefill GEMM family (force_path); the kernel that ran
-// is reported as PATH_GEMMW (register-operand 32x32x16 GEMM) or PATH_TILED
-// (the 16x16x32 fallback).
+// is reported as PATH_GEMMW (register-operand 32x32x16 GEMM), PATH_GEMMW_SPLIT
+// (the same with K split over workgroups) or PATH_TILED (the 16x16x32 fallback).
 enum Path {
   PATH_AUTO = 0, PATH_TILED = 2, PATH_GENERIC = 3, PATH_VECMAT_KN = 4, PATH_DECODE = 6, PATH_ROWS = 7,
-  PATH_GEMMW = 8, PATH_VECMAT32 = 9
+  PATH_GEMMW = 8, PATH_VECMAT32 = 9, PATH_GEMMW_SPLIT = 10
 };
 // prefill GEMM choice (gemm_impl): 0 the register-operand 32x32x16 kernel
 // where it takes the shape, 1 always the 16x16x32 tiled kernel
 std::atomic<int> g_gemm_impl{0};
+// gemm_split: 1 lets the 32x32x16 kernel split K over workgroups where its
+// tiles leave CUs idle, 0 keeps one workgroup per tile
+std::atomic<int> g_gemm_split{1};
 
 mq::GemvTuning gemv_tuning() {
   mq::GemvTuning t;
@@ -122,7 +125,7 @@ bool prefill_ok(const mq::LinearArgs& a) {
   return mq::gemmw_supported(a, num_cus_current()) || mq::tiled_supported(a);
 }
 
-int choose_path(const mq::LinearArgs& a) {
+int choose_path(const mq::LinearArgs& a, bool noalloc) {
   int forced = g_force_path.load();
   if (forced == PATH_ROWS && rows_ok(a)) return PATH_ROWS;
   if (forced == PATH_DECODE && decode_ok(a)) return PATH_DECODE;
@@ -137,6 +140,13 @@ int choose_path(const mq::LinearArgs& a) {
     const mq::RowsPlan pl = mq::rows_plan(a, num_cus_current());
     if (pl.ok && pl.KP == 1) return PATH_ROWS;
   }
+  // M = 13..16 with long rows: the prefill GEMM with K split over
+  // workgroups beats the split-K GEMV (measured at K >= 8192: 5 of 7 shapes
+  // faster by 4-38 %, e.g. K = 18944, N = 3584, M = 16: 31.6 vs 40.0 us; the
+  // exception, K = 8192, N = 4096, 5 % slower)
+  if (a.M >= 13 && a.K >= 8192 && !noalloc && g_gemm_impl.load() == 0 && g_gemm_split.load() != 0 &&
+      mq::gemmw_supported(a, num_cus_current()) && mq::gemmw_ws_bytes(a, num_cus_current(), true) > 0)
+    return PATH_TILED;
   if (decode_ok(a)) return PATH_DECODE;
   if (prefill_ok(a)) return PATH_TILED;
   return PATH_GENERIC;
@@ -145,7 +155,7 @@ int choose_path(const mq::LinearArgs& a) {
 // noalloc: the split-K GEMV uses the library's fixed scratch array instead of
 // the per-stream workspace (no allocation on any path).
 int run_linear(const mq::LinearArgs& a, hipStream_t s, bool noalloc = false) {
-  int path = choose_path(a);
+  int path = choose_path(a, noalloc);
   hipError_t e = hipSuccess;
   if (path == PATH_ROWS) {
     // K parts need the workspace: the no-allocation entry point takes the
@@ -186,14 +196,24 @@ int run_linear(const mq::LinearArgs& a, hipStream_t s, bool noalloc = false) {
     e = mq::gemv_launch(a, pl, ws, s);
   } else if (path == PATH_TILED) {
     const int impl = g_gemm_impl.load();
+    // K split over workgroups needs the per-stream workspace: the
+    // no-allocation entry point keeps one workgroup per tile
+    auto gemmw = [&]() -> hipError_t {
+      const int cus = num_cus_current();
+      const bool split = !noalloc && g_gemm_split.load() != 0;
+      void* ws = nullptr;
+      const size_t need = split ? mq::gemmw_ws_bytes(a, cus, true) : 0;
+      hipError_t we = workspace_for(s, need, &ws);
+      if (we != hipSuccess) return we;
+      path = need ? PATH_GEMMW_SPLIT : PATH_GEMMW;
+      return mq::gemmw_launch(a, cus, ws, s, split);
+    };
     if (impl == 0 && mq::gemmw_supported(a, num_cus_current())) {
-      e = mq::gemmw_launch(a, num_cus_current(), s);
-      path = PATH_GEMMW;
+      e = gemmw();
     } else if (mq::tiled_supported(a)) {
       e = mq::tiled_launch(a, s);
     } else if (mq::gemmw_supported(a, num_cus_current())) {
-      e = mq::gemmw_launch(a, num_cus_current(), s);
-      path = PATH_GEMMW;
+      e = gemmw();
     } else {
       e = mq::generic_linear_launch(a, s);
       path = PATH_GENERIC;
@@ -201,6 +221,9 @@ int run_linear(const mq::LinearArgs& a, hipStream_t s, bool noalloc = false) {
   } else {
     e = mq::generic_linear_launch(a, s);
   }
+  if (e == hipErrorStreamCaptureUnsupported)
+    return fail(MQ_INVALID_ARGUMENT, "dequant_matmul: the split-K workspace of this stream is too small; "
+                                     "make one call of this shape on the stream before capturing it");
   if (e != hipSuccess) return hip_fail(e, "dequant_matmul: kernel launch failed");
   g_last_path = path;
   return MQ_SUCCESS;
@@ -431,7 +454,7 @@ MQ_API int mq_vecmat_f16(const void* a, int64_t lda, const void* b, int64_t ldb,
   la.g = 1; la.G = 1;
   la.fmt = mq::FMT_F16;
   la.epi = mq::EPI_NONE;
-  const int pth = choose_path(la);
+  const int pth = choose_path(la, false);
   if (pth == PATH_DECODE || pth == PATH_ROWS) return run_linear(la, (hipStream_t)stream);
   hipError_t e = mq::generic_linear_launch(la, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "matmul: kernel launch failed");
@@ -556,6 +579,11 @@ MQ_API int mq_set_option(const char* key, int64_t value) {
   if (std::strcmp(key, "gemm_impl") == 0) {
     if (value != 0 && value != 1) return fail(MQ_INVALID_ARGUMENT, "set_option: gemm_impl must be 0 or 1");
     g_gemm_impl.store((int)value);
+    return MQ_SUCCESS;
+  }
+  if (std::strcmp(key, "gemm_split") == 0) {
+    if (value != 0 && value != 1) return fail(MQ_INVALID_ARGUMENT, "set_option: gemm_split must be 0 or 1");
+    g_gemm_split.store((int)value);
     return MQ_SUCCESS;
   }
   if (std::strcmp(key, "gemv_steps") == 0) {

@@ -69,6 +69,9 @@ struct GemmWArgs {
   int BN;            // output columns per tile (SwiGLU: gate columns)
   int nbm, nbn, xcd_remap;
   int KT;            // K-tiles
+  int KP, tiles;     // K parts (workgroups per tile) and output tiles
+  float* part;       // K > 1 parts: [KP][tiles][MB*NB blocks][1024] fp32 partial sums
+  uint32_t* cnt;     // K > 1 parts: per-tile arrival counts, zero between launches
   uint32_t a_bytes, w_bytes, s_bytes, z_bytes;
 };
 
@@ -79,13 +82,6 @@ struct WTile {            // one K-tile of one weight column for this lane half
 
 __device__ __forceinline__ void lds_dma16(rsrc_t r, u4* lds, uint32_t voff, uint32_t soff) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
-}
-
-// group range [g0, g0 + n) of the K-tiles [kt0, kt1) (gshift 31: one group per row)
-__host__ __device__ inline void wave_groups(int kt0, int kt1, int gshift, int& g0, int& n) {
-  if (gshift >= 31 || kt1 <= kt0) { g0 = 0; n = 1; return; }
-  g0 = (kt0 * KTK) >> gshift;
-  n = (((kt1 * KTK) - 1) >> gshift) - g0 + 1;
 }
 
 template <int FMT, bool SWI, int MB, int NB>
@@ -110,7 +106,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const int per = gridDim.x >> 3;
     id = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
   }
-  const int nb = id / p.nbm, mb = id - nb * p.nbm;
+  // K part major: the workgroups of one XCD share a K range of the activations
+  const int kp = p.KP > 1 ? id / p.tiles : 0;
+  const int otile = id - kp * p.tiles;   // output tile
+  const int nb = otile / p.nbm, mb = otile - nb * p.nbm;
   const int m0 = mb * 32 * MB;
   const int n0 = nb * p.BN;
 
@@ -120,7 +119,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   const rsrc_t zr = make_rsrc(p.zeros, p.z_bytes);
 
   // ---- this wave's K-tiles ----
-  const int kt0 = (w * p.KT) / NWV, kt1 = ((w + 1) * p.KT) / NWV;
+  const int kb = (kp * p.KT) / p.KP, ke = ((kp + 1) * p.KT) / p.KP;   // this K part
+  const int kt0 = kb + (w * (ke - kb)) / NWV, kt1 = kb + ((w + 1) * (ke - kb)) / NWV;
 
   // ---- activations: DMA into LDS, fully coalesced ----
   // Load instruction i moves rows 8i..8i+7 of the tile: lane l takes row
@@ -383,6 +383,56 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   constexpr int NBLK = SWI ? 2 : 1;          // blocks per unit
   constexpr int NU = MB * NB / NBLK;         // units
   const int rbase = m0 + 4 * h;
+  // epilogue and fp16 stores of unit (i, jq) from its fp32 sums
+  auto emit = [&](int i, int jq, const f16v (&sum)[SWI ? 2 : 1]) {
+    // lane holds D[row = 8*(v/4) + 4*h + v%4][col = r] of the block; the
+    // rows are checked against M only in the last M block, and the
+    // epilogue kind is switched on once per block
+    const int c = 32 * jq + r;
+    const int col = n0 + c;
+    const int row0 = rbase + 32 * i;
+    if (c >= p.BN || col >= (SWI ? p.F : p.N)) return;
+    _Float16* cp = p.C + (int64_t)row0 * p.ldc + col;
+    float outv[16];
+    if (SWI) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) outv[v] = silu_f32((float)(_Float16)sum[0][v]) * (float)(_Float16)sum[NBLK - 1][v];
+    } else {
+      const int kind = p.ep.epi;
+      const float bv = epi_needs_bias(kind) ? (float)((const _Float16*)p.ep.bias)[col] : 0.0f;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) outv[v] = sum[0][v] + bv;
+      if (kind == EPI_RESIDUAL) {
+        const _Float16* rp = (const _Float16*)p.ep.resid + (int64_t)row0 * p.ep.ldr + col;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int dr = 8 * (v >> 2) + (v & 3);
+          if (row0 + dr < p.M) outv[v] += (float)rp[(int64_t)dr * p.ep.ldr];
+        }
+      } else if (kind == EPI_BIAS_SILU) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) outv[v] = silu_f32(outv[v]);
+      } else if (kind == EPI_BIAS_RELU) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) outv[v] = fmaxf(outv[v], 0.0f);
+      }
+    }
+    if (m0 + 32 * (i + 1) <= p.M) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) cp[(int64_t)(8 * (v >> 2) + (v & 3)) * p.ldc] = (_Float16)outv[v];
+    } else {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int dr = 8 * (v >> 2) + (v & 3);
+        if (row0 + dr < p.M) cp[(int64_t)dr * p.ldc] = (_Float16)outv[v];
+      }
+    }
+  };
+  // partial sums of K part q, block blk of this tile: 16 values per lane,
+  // value v of lane l at float 64 v + l (coalesced)
+  auto part_of = [&](int q, int blk) -> float* {
+    return p.part + (((int64_t)q * p.tiles + otile) * (MB * NB) + blk) * kBlockF + lane;
+  };
   auto finish = [&](auto wc) {
     constexpr int W = decltype(wc)::value;
 #pragma unroll
@@ -420,49 +470,55 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
           }
         }
       }
-      // lane holds D[row = 8*(v/4) + 4*h + v%4][col = r] of the block; the
-      // rows are checked against M only in the last M block, and the
-      // epilogue kind is switched on once per block
-      const int c = 32 * jq + r;
-      const int col = n0 + c;
-      const int row0 = rbase + 32 * i;
-      if (c >= p.BN || col >= (SWI ? p.F : p.N)) continue;
-      _Float16* cp = p.C + (int64_t)row0 * p.ldc + col;
-      float outv[16];
-      if (SWI) {
+      if (p.KP == 1) {
+        emit(i, jq, sum);
+      } else {   // this K part's sums
 #pragma unroll
-        for (int v = 0; v < 16; ++v) outv[v] = silu_f32((float)(_Float16)sum[0][v]) * (float)(_Float16)sum[NBLK - 1][v];
-      } else {
-        const int kind = p.ep.epi;
-        const float bv = epi_needs_bias(kind) ? (float)((const _Float16*)p.ep.bias)[col] : 0.0f;
+        for (int b = 0; b < NBLK; ++b) {
+          float* dst = part_of(kp, i * NB + NBLK * jq + b);
 #pragma unroll
-        for (int v = 0; v < 16; ++v) outv[v] = sum[0][v] + bv;
-        if (kind == EPI_RESIDUAL) {
-          const _Float16* rp = (const _Float16*)p.ep.resid + (int64_t)row0 * p.ep.ldr + col;
-#pragma unroll
-          for (int v = 0; v < 16; ++v) {
-            const int dr = 8 * (v >> 2) + (v & 3);
-            if (row0 + dr < p.M) outv[v] += (float)rp[(int64_t)dr * p.ep.ldr];
-          }
-        } else if (kind == EPI_BIAS_SILU) {
-#pragma unroll
-          for (int v = 0; v < 16; ++v) outv[v] = silu_f32(outv[v]);
-        } else if (kind == EPI_BIAS_RELU) {
-#pragma unroll
-          for (int v = 0; v < 16; ++v) outv[v] = fmaxf(outv[v], 0.0f);
-        }
-      }
-      if (m0 + 32 * (i + 1) <= p.M) {
-#pragma unroll
-        for (int v = 0; v < 16; ++v) cp[(int64_t)(8 * (v >> 2) + (v & 3)) * p.ldc] = (_Float16)outv[v];
-      } else {
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int dr = 8 * (v >> 2) + (v & 3);
-          if (row0 + dr < p.M) cp[(int64_t)dr * p.ldc] = (_Float16)outv[v];
+          for (int v = 0; v < 16; ++v)
+            __hip_atomic_store(dst + 64 * v, sum[b][v], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
         }
       }
     }
+    if (p.KP == 1) return;
+    // Split K: the last of the tile's K parts to arrive sums all parts in
+    // part order (deterministic) and stores; no workgroup waits for another.
+    // Ordering: every access to the partials is a system-scope atomic
+    // (stores written through to memory, loads served from memory); each
+    // wave waits for its stores to be acknowledged before the barrier that
+    // precedes the count, so the count is taken only after every partial of
+    // this part is in memory.  That is the gfx950 lowering of a system-scope
+    // release (and, on the reading side, acquire) without the L2 writeback
+    // and invalidate, which exist to publish non-atomic accesses (none are
+    // made here) and measured 2-3x slower for this kernel as a whole.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();   // also: every wave is done with the reduction slots
+    uint32_t* flag = (uint32_t*)&lds_s[0];
+    if (tid == 0) {
+      const uint32_t prev = __hip_atomic_fetch_add(p.cnt + otile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      *flag = prev == (uint32_t)(p.KP - 1) ? 1u : 0u;
+    }
+    __syncthreads();
+    if (*flag == 0u) return;
+#pragma unroll
+    for (int u = W; u < NU; u += 4) {
+      const int i = u / (NB / NBLK), jq = u - i * (NB / NBLK);
+      f16v sum[NBLK];
+#pragma unroll
+      for (int b = 0; b < NBLK; ++b) {
+        sum[b] = (f16v){};
+        for (int q = 0; q < p.KP; ++q) {
+          const float* src = part_of(q, i * NB + NBLK * jq + b);
+#pragma unroll
+          for (int v = 0; v < 16; ++v)
+            sum[b][v] += __hip_atomic_load(src + 64 * v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        }
+      }
+      emit(i, jq, sum);
+    }
+    if (tid == 0) __hip_atomic_store(p.cnt + otile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);   // for the next launch
   };
   switch (w) {
     case 0: finish(std::integral_constant<int, 0>{}); break;
@@ -475,9 +531,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 // ---- host side: tile planning and launch ----
 
 struct WPlan {
-  int MB, NB, BN, nbm, nbn;
+  int MB, NB, BN, nbm, nbn, KP;
+  size_t ws_bytes;
   bool ok;
 };
+
+constexpr size_t kCntBytesW = 65536;   // per-tile counters at the start of the workspace
 
 int gshift_of(const LinearArgs& a) {
   if (a.G == 1) return 31;
@@ -495,7 +554,7 @@ bool sz_table_fits(const LinearArgs& a, int BN) {
 // VALU, texture-unit requests and the tile's weight bytes at its share of
 // ~6 TB/s; the launch takes ceil(tiles / CUs) tile times (one workgroup per
 // CU).
-WPlan plan(const LinearArgs& a, int cus) {
+WPlan plan(const LinearArgs& a, int cus, bool allow_split) {
   WPlan best{};
   best.ok = false;
   double best_t = 1e300;
@@ -530,11 +589,49 @@ WPlan plan(const LinearArgs& a, int cus) {
         const double t = std::ceil((double)tiles / cus) * std::max(std::max(t_mfma, t_ta), std::max(t_valu, t_mem));
         if (t < best_t * 0.999) {
           best_t = t;
-          best = WPlan{MB, NB, BN, nbm, nbn, true};
+          best = WPlan{MB, NB, BN, nbm, nbn, 1, 0, true};
         }
       }
     }
   }
+  // K split over workgroups, where the tiles above leave at least half the
+  // CUs idle: candidates of 2 weight blocks (wider tiles measured slower at
+  // these shapes) with 1..8 K parts of at least 8 K-tiles each, priced by a
+  // launch-time model fitted to 290 measured launches (int4, M = 17..128, K
+  // = 2048..18944): per-wave K-tiles times the tile's MFMA, dequant and
+  // activation work, rounds of workgroups over the CUs, and for K parts a
+  // fixed cost plus the last arriver's reads of the parts.
+  if (best.ok && allow_split && (int64_t)best.nbm * best.nbn * 2 <= cus) {
+    auto fitted = [&](int MB, int NB, int64_t tiles, int KP) {
+      const double per = kt / KP / 4.0;
+      const double rounds = std::ceil((double)(tiles * KP) / cus);
+      const double rp = rounds * per;
+      const double sp = KP > 1 ? 1.0 : 0.0;
+      return -5.09 + rp * (0.1544 + 0.1768 * MB * NB + 0.0858 * NB - 0.1602 * MB) + sp * (2.78 + 0.1575 * KP * MB * NB) +
+             11.39 * rounds;
+    };
+    double fbest = fitted(best.MB, best.NB, (int64_t)best.nbm * best.nbn, 1);
+    const int NB = 2;
+    for (int MB : mbs) {
+      if (MB == 2 && a.M > 96) continue;
+      for (int BN = (swi ? 16 : 32) * NB - 16; BN <= (swi ? 16 : 32) * NB; BN += 16) {
+        if (BN <= 0 || !sz_table_fits(a, BN)) continue;
+        const int nbm = (a.M + 32 * MB - 1) / (32 * MB);
+        const int nbn = (ncols + BN - 1) / BN;
+        const int64_t tiles = (int64_t)nbm * nbn;
+        if (tiles * 4 > (int64_t)kCntBytesW) continue;
+        for (int KP = 2; KP <= 8 && tiles * KP <= cus && kt >= 8.0 * KP; ++KP) {
+          const double f = fitted(MB, NB, tiles, KP);
+          if (f < fbest * 0.999) {
+            fbest = f;
+            best = WPlan{MB, NB, BN, nbm, nbn, KP, 0, true};
+          }
+        }
+      }
+    }
+  }
+  if (best.ok && best.KP > 1)
+    best.ws_bytes = kCntBytesW + (size_t)best.KP * best.nbm * best.nbn * best.MB * best.NB * kBlockF * 4;
   return best;
 }
 
@@ -580,12 +677,15 @@ bool gemmw_supported(const LinearArgs& a, int cus) {
   const int64_t lim = (int64_t)1 << 31;
   if (((int64_t)(a.M - 1) * a.lda + a.K) * 2 >= lim) return false;
   if ((int64_t)a.N * a.ldw >= lim || (int64_t)a.N * a.G * 2 >= lim) return false;
-  return plan(a, cus).ok;
+  return plan(a, cus, false).ok;
 }
 
-hipError_t gemmw_launch(const LinearArgs& a, int cus, hipStream_t s) {
-  const WPlan pl = plan(a, cus);
+size_t gemmw_ws_bytes(const LinearArgs& a, int cus, bool allow_split) { return plan(a, cus, allow_split).ws_bytes; }
+
+hipError_t gemmw_launch(const LinearArgs& a, int cus, void* ws, hipStream_t s, bool allow_split) {
+  const WPlan pl = plan(a, cus, allow_split);
   if (!pl.ok) return hipErrorInvalidValue;
+  if (pl.KP > 1 && !ws) return hipErrorInvalidValue;
   GemmWArgs k{};
   k.A = (const _Float16*)a.A; k.lda = a.lda;
   k.W = (const unsigned char*)a.W; k.ldw = a.ldw;
@@ -596,7 +696,13 @@ hipError_t gemmw_launch(const LinearArgs& a, int cus, hipStream_t s) {
   k.gshift = gshift_of(a);
   k.BN = pl.BN; k.nbm = pl.nbm; k.nbn = pl.nbn;
   k.KT = (a.K + KTK - 1) / KTK;
-  const int nwg = pl.nbm * pl.nbn;
+  k.KP = pl.KP;
+  k.tiles = pl.nbm * pl.nbn;
+  if (pl.KP > 1) {
+    k.cnt = (uint32_t*)ws;
+    k.part = (float*)((char*)ws + kCntBytesW);
+  }
+  const int nwg = k.tiles * pl.KP;
   k.xcd_remap = (nwg % 8 == 0) ? 1 : 0;
   k.a_bytes = (uint32_t)(((int64_t)(a.M - 1) * a.lda + a.K) * 2);
   k.w_bytes = (uint32_t)((int64_t)a.N * a.ldw);

@@ -97,9 +97,13 @@ struct RowsPlan {
 RowsPlan rows_plan(const LinearArgs& a, int num_cus, bool allow_split = true);
 hipError_t rows_launch(const LinearArgs& a, const RowsPlan& p, void* ws, hipStream_t s);
 
-// Register-operand 32x32x16 MFMA GEMM (prefill default).
+// Register-operand 32x32x16 MFMA GEMM (prefill default).  Where its tiles
+// leave CUs idle it may split K over several workgroups per tile (only when
+// allow_split), which needs a zeroed workspace of gemmw_ws_bytes (counters
+// that every launch leaves at zero, then the partial sums).
 bool gemmw_supported(const LinearArgs& a, int num_cus);
-hipError_t gemmw_launch(const LinearArgs& a, int num_cus, hipStream_t s);
+size_t gemmw_ws_bytes(const LinearArgs& a, int num_cus, bool allow_split);
+hipError_t gemmw_launch(const LinearArgs& a, int num_cus, void* ws, hipStream_t s, bool allow_split);
 
 // 16x16x32 MFMA GEMM, K steps of 32 (fallback for shapes the GEMM above does not take).
 bool tiled_supported(const LinearArgs& a);

@@ -28,7 +28,7 @@ GOLD = os.path.join(os.path.dirname(__file__), "golden", "known_answers.npz")
 PATHS = {"tiled": 2, "generic": 3, "decode": 6, "rows": 7}
 # force_path "tiled" selects the prefill GEMM family; the kernel that ran is
 # reported as "gemmw" (register-operand GEMM) or "tiled" (16x16x32 fallback)
-FAMILY = {"gemmw": "tiled"}
+FAMILY = {"gemmw": "tiled", "gemmw_split": "tiled"}
 
 
 @pytest.fixture(scope="module")
@@ -241,6 +241,25 @@ def test_config2_qwen7b_down(mn, gpu, M):
             continue  # activations do not fit in LDS at this M
         assert taken == path
         check_close(y, ref, f"config2 M={M} [{path}, {mn.last_path()}]")
+
+
+@pytest.mark.parametrize("M,K,N,want", [(16, 18944, 3584, "gemmw_split"), (12, 18944, 3584, "decode"),
+                                         (16, 4096, 4096, "decode"), (32, 18944, 3584, "gemmw_split")])
+def test_mid_band_routing(mn, gpu, M, K, N, want):
+    """Between the decode GEMVs and the prefill GEMM: at M = 13..16 with K >=
+    8192 the prefill GEMM with K split over workgroups is taken where it
+    splits; the result matches the oracle on every path."""
+    say(f"mid band M={M} K={K} N={N}")
+    g = 128
+    x, wp, s, z = O.make_int4_problem(M, K, N, g, seed=M)
+    ref = O.matmul_f32acc(x, O.dequant_int4(wp, s, z, K, g))
+    y, _ = run_dm(mn, gpu, x, wp, s, z, g, "int4", None)
+    assert mn.last_path() == want, mn.last_path()
+    check_close(y, ref, f"mid band auto [{want}]")
+    if M <= 16:
+        y2, taken = run_dm(mn, gpu, x, wp, s, z, g, "int4", "decode")
+        assert taken == "decode"
+        check_close(y2, ref, "mid band decode")
 
 
 def test_config1_qwen05b_gate(mn, gpu):
@@ -744,6 +763,55 @@ def test_prefill_gemm_kernels(mn, gpu, impl, qt, g, epi, M, K, N):
         check_close(y, acc, f"gemm impl={impl}")
     else:
         check_epilogue(y, acc, epi, f"gemm impl={impl} {epi}", bias=b, residual=res)
+
+
+@pytest.mark.parametrize("qt,g,epi", [("int4", 128, None), ("int4", 32, "bias"), ("int4", 64, "swiglu"),
+                                      ("int8", 0, "residual"), ("int8", 64, "bias_relu")])
+@pytest.mark.parametrize("M,K,N", [(17, 4096, 512), (64, 3104, 256), (33, 4096, 96), (100, 4096, 320)])
+def test_prefill_gemm_split_k(mn, gpu, qt, g, epi, M, K, N):
+    """Shapes whose output tiles would leave most CUs idle: the 32x32x16
+    kernel splits K over several workgroups per tile and the last part to
+    arrive sums the parts in part order.  Checked against the oracle, run
+    twice for bit-identical results (a fixed summation order), and against
+    the same kernel with the split switched off (one workgroup per tile)."""
+    say(f"gemm split {qt} g={g} {epi} M={M} K={K} N={N}")
+    if qt == "int4":
+        x, wp, s, z = O.make_int4_problem(M, K, N, g, seed=M + K + N)
+        acc = O.matmul_f32acc(x, O.dequant_int4(wp, s, z, K, g))
+    else:
+        x, wp, s, z, g = O.make_int8_problem(M, K, N, seed=M + K + N, g=g or None)
+        acc = O.matmul_f32acc(x, O.dequant_int8(wp, s, z, K, g))
+    kw, b, res = {}, None, None
+    if epi in ("bias", "bias_relu"):
+        b = np.random.default_rng(N).standard_normal(N).astype(np.float16)
+        kw = {"epilogue": epi, "bias": dev(b, gpu)}
+    elif epi == "residual":
+        res = np.random.default_rng(M).standard_normal((M, N)).astype(np.float16)
+        kw = {"epilogue": "residual", "residual": dev(res, gpu)}
+    elif epi == "swiglu":
+        kw = {"epilogue": "swiglu"}
+
+    def check(y, what):
+        if epi == "swiglu":
+            check_swiglu(y, acc, what)
+        elif epi is None:
+            check_close(y, acc, what)
+        else:
+            check_epilogue(y, acc, epi, what, bias=b, residual=res)
+
+    y, taken = run_dm(mn, gpu, x, wp, s, z, g, qt, "tiled", **kw)
+    assert mn.last_path() == "gemmw_split", mn.last_path()
+    check(y, "gemm split")
+    y2, _ = run_dm(mn, gpu, x, wp, s, z, g, qt, "tiled", **kw)
+    np.testing.assert_array_equal(y2.view(np.uint16), y.view(np.uint16))
+    mn.set_option("gemm_split", 0)
+    try:
+        y1, _ = run_dm(mn, gpu, x, wp, s, z, g, qt, "tiled", **kw)
+        ran = mn.last_path()
+    finally:
+        mn.set_option("gemm_split", 1)
+    assert ran == "gemmw", ran
+    check(y1, "gemm one part per tile")
 
 
 @pytest.mark.parametrize("path,M,K,N,g,qt,impl", [
