@@ -596,7 +596,7 @@ WPlan plan(const LinearArgs& a, int cus, bool allow_split) {
   }
   // K split over workgroups, where the tiles above leave at least half the
   // CUs idle: candidates of 2 weight blocks (wider tiles measured slower at
-  // these shapes) with 1..8 K parts of at least 8 K-tiles each, priced by a
+  // these shapes) and 1, 2 or 4 A blocks, with 1..8 K parts of at least 8 K-tiles each, priced by a
   // launch-time model fitted to 290 measured launches (int4, M = 17..128, K
   // = 2048..18944): per-wave K-tiles times the tile's MFMA, dequant and
   // activation work, rounds of workgroups over the CUs, and for K parts a
@@ -612,8 +612,10 @@ WPlan plan(const LinearArgs& a, int cus, bool allow_split) {
     };
     double fbest = fitted(best.MB, best.NB, (int64_t)best.nbm * best.nbn, 1);
     const int NB = 2;
-    for (int MB : mbs) {
-      if (MB == 2 && a.M > 96) continue;
+    // one A block per tile where M <= 32 (12-17 % faster than two at M = 16..32)
+    const int smbs[3] = {4, 2, 1};
+    for (int MB : smbs) {
+      if ((MB == 2 && a.M > 96) || (MB == 1 && a.M > 32)) continue;
       for (int BN = (swi ? 16 : 32) * NB - 16; BN <= (swi ? 16 : 32) * NB; BN += 16) {
         if (BN <= 0 || !sz_table_fits(a, BN)) continue;
         const int nbm = (a.M + 32 * MB - 1) / (32 * MB);
@@ -644,7 +646,9 @@ hipError_t launch4(const GemmWArgs& k, int nwg, hipStream_t s) {
 // instantiated tile shapes: MB * NB <= 12 (accumulator registers)
 template <int FMT, bool SWI, int MB>
 hipError_t launch3(const GemmWArgs& k, int NB, int nwg, hipStream_t s) {
-  if constexpr (MB == 4) {
+  if constexpr (MB == 1) {
+    if (NB == 2) return launch4<FMT, SWI, 1, 2>(k, nwg, s);
+  } else if constexpr (MB == 4) {
     if (NB == 2) return launch4<FMT, SWI, 4, 2>(k, nwg, s);
     if constexpr (!SWI) {
       if (NB == 3) return launch4<FMT, SWI, 4, 3>(k, nwg, s);
@@ -662,7 +666,9 @@ hipError_t launch3(const GemmWArgs& k, int NB, int nwg, hipStream_t s) {
 
 template <int FMT, bool SWI>
 hipError_t launch2(const GemmWArgs& k, const WPlan& pl, int nwg, hipStream_t s) {
-  return pl.MB == 4 ? launch3<FMT, SWI, 4>(k, pl.NB, nwg, s) : launch3<FMT, SWI, 2>(k, pl.NB, nwg, s);
+  if (pl.MB == 4) return launch3<FMT, SWI, 4>(k, pl.NB, nwg, s);
+  if (pl.MB == 2) return launch3<FMT, SWI, 2>(k, pl.NB, nwg, s);
+  return launch3<FMT, SWI, 1>(k, pl.NB, nwg, s);
 }
 
 }  // namespace
