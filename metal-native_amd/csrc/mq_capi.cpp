@@ -140,11 +140,12 @@ int choose_path(const mq::LinearArgs& a, bool noalloc) {
     const mq::RowsPlan pl = mq::rows_plan(a, num_cus_current());
     if (pl.ok && pl.KP == 1) return PATH_ROWS;
   }
-  // M = 13..16 with long rows: the prefill GEMM with K split over
-  // workgroups beats the split-K GEMV (measured at K >= 8192 on 6 shapes,
-  // faster by 10-45 %, e.g. K = 18944, N = 3584, M = 16: 26.3 vs 40.0 us;
-  // at K = 4096, N = 4096 it is 8 % slower, hence the K bound)
-  if (a.M >= 13 && a.K >= 8192 && !noalloc && g_gemm_impl.load() == 0 && g_gemm_split.load() != 0 &&
+  // M = 9..16 with long rows: the prefill GEMM with K split over
+  // workgroups beats the split-K GEMV (measured at K >= 8192 on 6 shapes at
+  // M = 9, 12, 13-16: faster on all but K = 8192, N = 4096 (2-10 % slower
+  // at M = 9-16), by up to 45 %, e.g. K = 18944, N = 3584, M = 16: 26.3 vs
+  // 40.0 us; at K = 4096, N = 4096 it is 8 % slower, hence the K bound)
+  if (a.M >= 9 && a.K >= 8192 && !noalloc && g_gemm_impl.load() == 0 && g_gemm_split.load() != 0 &&
       mq::gemmw_supported(a, num_cus_current()) && mq::gemmw_ws_bytes(a, num_cus_current(), true) > 0)
     return PATH_TILED;
   if (decode_ok(a)) return PATH_DECODE;

@@ -243,10 +243,11 @@ def test_config2_qwen7b_down(mn, gpu, M):
         check_close(y, ref, f"config2 M={M} [{path}, {mn.last_path()}]")
 
 
-@pytest.mark.parametrize("M,K,N,want", [(16, 18944, 3584, "gemmw_split"), (12, 18944, 3584, "decode"),
-                                         (16, 4096, 4096, "decode"), (32, 18944, 3584, "gemmw_split")])
+@pytest.mark.parametrize("M,K,N,want", [(16, 18944, 3584, "gemmw_split"), (9, 18944, 3584, "gemmw_split"),
+                                         (8, 18944, 3584, "decode"), (16, 4096, 4096, "decode"),
+                                         (32, 18944, 3584, "gemmw_split")])
 def test_mid_band_routing(mn, gpu, M, K, N, want):
-    """Between the decode GEMVs and the prefill GEMM: at M = 13..16 with K >=
+    """Between the decode GEMVs and the prefill GEMM: at M = 9..16 with K >=
     8192 the prefill GEMM with K split over workgroups is taken where it
     splits; the result matches the oracle on every path."""
     say(f"mid band M={M} K={K} N={N}")
