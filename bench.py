@@ -82,6 +82,9 @@ CONFIGS = {
     "cfg4_qwen7b_gateup_int8_swiglu_m1": ("int8", 1, 3584, 2 * 18944, 3584, "swiglu", "hbm"),
     "cfg4_qwen7b_gateup_int8_swiglu_m16": ("int8", 16, 3584, 2 * 18944, 3584, "swiglu", "hbm"),
     "cfg4_qwen7b_gateup_int8_swiglu_m64": ("int8", 64, 3584, 2 * 18944, 3584, "swiglu", "hbm"),
+    # the band between decode and prefill at the config-2 shape (not a baseline config)
+    "midband_qwen7b_down_m16": ("int4", 16, 18944, 3584, 128, None, "hbm"),
+    "midband_qwen7b_down_m32": ("int4", 32, 18944, 3584, 128, None, "hbm"),
 }
 HEADLINE = "cfg2_qwen7b_down_m1"
 
