@@ -562,13 +562,17 @@ WPlan plan(const LinearArgs& a, int cus, bool allow_split) {
   const int ncols = swi ? a.F : a.N;
   const double kt = std::ceil(a.K / 64.0);
   const double bpw = a.fmt == FMT_INT4 ? 0.5 : 1.0;
-  const int mbs[2] = {4, 2};
+  // 4 A blocks per weight block keep the dequant VALU in the MFMA shadow;
+  // fewer only for few rows (one block of 32 rows: M <= 32, measured 17 %
+  // faster than two at M = 32, K = 3584, N = 14336)
+  const int mbs[3] = {4, 2, 1};
   for (int MB : mbs) {
-    if (MB == 2 && a.M > 96) continue;   // 4 A blocks per weight block keep the dequant VALU in the MFMA shadow
+    if ((MB == 2 && a.M > 96) || (MB == 1 && a.M > 32)) continue;
     for (int NB = 2; NB <= 6; ++NB) {
       if (swi && NB % 2) continue;
       // the instantiated shapes (launch3); MB * NB <= 12 accumulator blocks
-      const bool inst = MB == 4 ? (NB == 2 || (NB == 3 && !swi)) : (NB == 2 || NB == 4 || NB == 6 || (NB == 3 && !swi));
+      const bool inst = MB == 4 ? (NB == 2 || (NB == 3 && !swi))
+                                : MB == 2 ? (NB == 2 || NB == 4 || NB == 6 || (NB == 3 && !swi)) : NB == 2;
       if (!inst) continue;
       const int maxbn = swi ? 16 * NB : 32 * NB;
       for (int BN = maxbn - 16; BN <= maxbn; BN += 16) {
@@ -613,8 +617,7 @@ WPlan plan(const LinearArgs& a, int cus, bool allow_split) {
     double fbest = fitted(best.MB, best.NB, (int64_t)best.nbm * best.nbn, 1);
     const int NB = 2;
     // one A block per tile where M <= 32 (12-17 % faster than two at M = 16..32)
-    const int smbs[3] = {4, 2, 1};
-    for (int MB : smbs) {
+    for (int MB : mbs) {
       if ((MB == 2 && a.M > 96) || (MB == 1 && a.M > 32)) continue;
       for (int BN = (swi ? 16 : 32) * NB - 16; BN <= (swi ? 16 : 32) * NB; BN += 16) {
         if (BN <= 0 || !sz_table_fits(a, BN)) continue;
