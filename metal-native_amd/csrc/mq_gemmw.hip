@@ -84,7 +84,9 @@ __device__ __forceinline__ void lds_dma16(rsrc_t r, u4* lds, uint32_t voff, uint
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
 }
 
-template <int FMT, bool SWI, int MB, int NB>
+// KS: K split over p.KP workgroups per tile (a separate instantiation, so
+// that the one-part kernel's code is not shaped by the split's epilogue)
+template <int FMT, bool SWI, int MB, int NB, bool KS>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemmw_kernel(GemmWArgs p) {
   // Activation slots (separate arrays, so that the compiler's load-counter
   // waits tell a slot's DMA from the other's) and the scale tables; after
@@ -107,8 +109,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     id = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
   }
   // K part major: the workgroups of one XCD share a K range of the activations
-  const int kp = p.KP > 1 ? id / p.tiles : 0;
-  const int otile = id - kp * p.tiles;   // output tile
+  const int kp = KS ? id / p.tiles : 0;
+  const int otile = KS ? id - kp * p.tiles : id;   // output tile
   const int nb = otile / p.nbm, mb = otile - nb * p.nbm;
   const int m0 = mb * 32 * MB;
   const int n0 = nb * p.BN;
@@ -119,7 +121,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   const rsrc_t zr = make_rsrc(p.zeros, p.z_bytes);
 
   // ---- this wave's K-tiles ----
-  const int kb = (kp * p.KT) / p.KP, ke = ((kp + 1) * p.KT) / p.KP;   // this K part
+  const int kb = KS ? (kp * p.KT) / p.KP : 0, ke = KS ? ((kp + 1) * p.KT) / p.KP : p.KT;   // this K part
   const int kt0 = kb + (w * (ke - kb)) / NWV, kt1 = kb + ((w + 1) * (ke - kb)) / NWV;
 
   // ---- activations: DMA into LDS, fully coalesced ----
@@ -470,7 +472,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
           }
         }
       }
-      if (p.KP == 1) {
+      if constexpr (!KS) {
         emit(i, jq, sum);
       } else {   // this K part's sums
 #pragma unroll
@@ -482,7 +484,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         }
       }
     }
-    if (p.KP == 1) return;
+    if constexpr (!KS) return;
     // Split K: the last of the tile's K parts to arrive sums all parts in
     // part order (deterministic) and stores; no workgroup waits for another.
     // Ordering: every access to the partials is a system-scope atomic
@@ -642,7 +644,16 @@ WPlan plan(const LinearArgs& a, int cus, bool allow_split) {
 
 template <int FMT, bool SWI, int MB, int NB>
 hipError_t launch4(const GemmWArgs& k, int nwg, hipStream_t s) {
-  hipLaunchKernelGGL((gemmw_kernel<FMT, SWI, MB, NB>), dim3(nwg), dim3(64 * NWV), 0, s, k);
+  // K parts are planned with 2 weight blocks per tile only
+  if constexpr (NB == 2) {
+    if (k.KP > 1) {
+      hipLaunchKernelGGL((gemmw_kernel<FMT, SWI, MB, NB, true>), dim3(nwg), dim3(64 * NWV), 0, s, k);
+      return hipGetLastError();
+    }
+  } else {
+    if (k.KP > 1) return hipErrorInvalidValue;
+  }
+  hipLaunchKernelGGL((gemmw_kernel<FMT, SWI, MB, NB, false>), dim3(nwg), dim3(64 * NWV), 0, s, k);
   return hipGetLastError();
 }
 
