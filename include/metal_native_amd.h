@@ -78,10 +78,14 @@ enum mq_epilogue {
  * itself when ldr == ldc (each element is read and then written by one
  * thread).  The kernels that split K across workgroups (the split-K GEMV,
  * the row-block GEMV when the activations exceed LDS, and the prefill GEMM
- * where its output tiles would leave most CUs idle) keep their partial sums and counters in a library workspace per (device,
- * stream), allocated by the first call on that stream that needs it (so that
- * call must not be inside stream capture).  Calls on one stream are ordered
- * and share it. */
+ * where its output tiles would leave most CUs idle) keep their partial sums
+ * and counters in a library workspace per (device, stream), allocated by the
+ * first call on that stream that needs it (so that call must not be inside
+ * stream capture; under capture the prefill GEMM then keeps one workgroup per
+ * tile instead).  Calls on one stream are ordered and share it.  When a
+ * larger shape needs more, a new workspace replaces it for later calls; the
+ * old one is kept (not freed) until the process ends, so graphs captured
+ * earlier on that stream stay valid. */
 MQ_API int mq_dequant_matmul(const void* activations, int64_t lda, const void* weights_packed,
                              int64_t ldw_bytes, const void* scales, const void* zeros, void* out,
                              int64_t ldc, int64_t M, int64_t N, int64_t K, int32_t group_size,
@@ -224,9 +228,11 @@ MQ_API int mq_argmax_embed_f16(const void* logits, int64_t vocab, const void* em
  * 3 generic, 6 split-K decode GEMV, 7 row-block decode GEMV), "gemv_steps"
  * (K steps per wavefront of the split-K GEMV, 1..8, 0 automatic),
  * "gemv_tiles_per_wg" (row tiles per workgroup: 1, 2 or 4, 0 automatic),
- * "gemm_impl" (prefill GEMM kernel: 0 the register-operand 32x32x16 kernel
- * where it takes the shape, 1 always the 16x16x32 tiled kernel; both compute
- * the same contract), "gemm_split" (1, the default: the 32x32x16 kernel splits
+ * "gemm_impl" (prefill GEMM kernel: 0 automatic -- the 128-row int4 GEMM
+ * where its tiles fill the GPU, else the register-operand 32x32x16 kernel
+ * where it takes the shape --, 1 always the 16x16x32 tiled kernel, 2 the
+ * 128-row int4 GEMM wherever it takes the shape; all compute the same
+ * contract), "gemm_split" (1, the default: the 32x32x16 kernel splits
  * K over several workgroups per output tile where its tiles would leave CUs
  * idle, summing the parts in a fixed order; 0: one workgroup per tile).  A forced path that cannot take the shape falls back
  * to the automatic choice.  Returns MQ_INVALID_ARGUMENT for an unknown key or
@@ -237,7 +243,7 @@ MQ_API int mq_set_option(const char* key, int64_t value);
  * mq_vecmat_f32 call on this thread launched: 2 16x16x32 tiled GEMM, 3
  * generic, 4 vecmat [K,N], 6 split-K decode GEMV, 7 row-block decode GEMV, 8
  * 32x32x16 prefill GEMM, 9 fp32 vecmat, 10 32x32x16 prefill GEMM with K split
- * over workgroups. */
+ * over workgroups, 11 128-row int4 prefill GEMM. */
 MQ_API int mq_last_path(void);
 
 MQ_API const char* mq_last_error(void);

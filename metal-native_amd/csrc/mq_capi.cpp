@@ -12,6 +12,7 @@
 #include <set>
 #include <string>
 #include <utility>
+#include <vector>
 
 #include "../../include/metal_native_amd.h"
 #include "mq_launch.hpp"
@@ -50,14 +51,17 @@ int num_cus_current() {
 // Path ids (mq_last_path / force_path); 1 and 5 are retired ids of earlier
 // decode kernels and are not reused.
 // PATH_TILED selects the prefill GEMM family (force_path); the kernel that ran
-// is reported as PATH_GEMMW (register-operand 32x32x16 GEMM), PATH_GEMMW_SPLIT
-// (the same with K split over workgroups) or PATH_TILED (the 16x16x32 fallback).
+// is reported as PATH_GEMM16 (the 128-row int4 GEMM), PATH_GEMMW
+// (register-operand 32x32x16 GEMM), PATH_GEMMW_SPLIT (the same with K split
+// over workgroups) or PATH_TILED (the 16x16x32 fallback).
 enum Path {
   PATH_AUTO = 0, PATH_TILED = 2, PATH_GENERIC = 3, PATH_VECMAT_KN = 4, PATH_DECODE = 6, PATH_ROWS = 7,
-  PATH_GEMMW = 8, PATH_VECMAT32 = 9, PATH_GEMMW_SPLIT = 10
+  PATH_GEMMW = 8, PATH_VECMAT32 = 9, PATH_GEMMW_SPLIT = 10, PATH_GEMM16 = 11
 };
-// prefill GEMM choice (gemm_impl): 0 the register-operand 32x32x16 kernel
-// where it takes the shape, 1 always the 16x16x32 tiled kernel
+// prefill GEMM choice (gemm_impl): 0 automatic (the 128-row int4 GEMM where
+// its tiles fill the GPU, else the register-operand 32x32x16 kernel where it
+// takes the shape), 1 always the 16x16x32 tiled kernel, 2 the 128-row int4
+// GEMM wherever it takes the shape
 std::atomic<int> g_gemm_impl{0};
 // gemm_split: 1 lets the 32x32x16 kernel split K over workgroups where its
 // tiles leave CUs idle, 0 keeps one workgroup per tile
@@ -83,6 +87,7 @@ struct Workspace {
 };
 std::mutex g_ws_mu;
 std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
+std::vector<void*> g_ws_retired;   // superseded workspaces: kept until the process ends
 
 hipError_t workspace_for(hipStream_t s, size_t need, void** out) {
   *out = nullptr;
@@ -97,13 +102,10 @@ hipError_t workspace_for(hipStream_t s, size_t need, void** out) {
     if (hipStreamIsCapturing(s, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
       return hipErrorStreamCaptureUnsupported;  // first call on this stream must be outside capture
     size_t nb = need < ((size_t)1 << 20) ? ((size_t)1 << 20) : need;
-    if (w.ptr) {
-      e = hipStreamSynchronize(s);  // the old buffer may still be in use on s
-      if (e != hipSuccess) return e;
-      (void)hipFree(w.ptr);
-      w.ptr = nullptr;
-      w.bytes = 0;
-    }
+    // A superseded buffer is kept, not freed: graphs captured earlier on
+    // this stream hold its address and may still be replayed.  Growth is
+    // geometric, so the retired buffers add up to less than the live one.
+    if (nb < 2 * w.bytes) nb = 2 * w.bytes;
     void* p = nullptr;
     e = hipMalloc(&p, nb);
     if (e != hipSuccess) return e;
@@ -112,6 +114,7 @@ hipError_t workspace_for(hipStream_t s, size_t need, void** out) {
     // capture: refused above)
     e = hipMemsetAsync(p, 0, nb, s);
     if (e != hipSuccess) { (void)hipFree(p); return e; }
+    if (w.ptr) g_ws_retired.push_back(w.ptr);
     w.ptr = p;
     w.bytes = nb;
   }
@@ -122,7 +125,17 @@ hipError_t workspace_for(hipStream_t s, size_t need, void** out) {
 bool rows_ok(const mq::LinearArgs& a) { return mq::rows_plan(a, num_cus_current()).ok; }
 
 bool prefill_ok(const mq::LinearArgs& a) {
-  return mq::gemmw_supported(a, num_cus_current()) || mq::tiled_supported(a);
+  return mq::gemm16_supported(a) || mq::gemmw_supported(a, num_cus_current()) || mq::tiled_supported(a);
+}
+
+// The 128-row int4 GEMM, automatically: where its tiles cover the CUs at
+// least three quarters of the way and its 128-row blocks are at least three
+// quarters full (config 3, M = 512: 256 tiles on 256 CUs).  Smaller grids go
+// to the 32x32x16 kernel, whose planner picks narrower tiles or splits K.
+bool gemm16_auto(const mq::LinearArgs& a) {
+  if (!mq::gemm16_supported(a)) return false;
+  const int64_t mpad = (int64_t)((a.M + 127) / 128) * 128;
+  return 4 * (int64_t)mq::gemm16_workgroups(a) >= 3 * (int64_t)num_cus_current() && 4 * (int64_t)a.M >= 3 * mpad;
 }
 
 int choose_path(const mq::LinearArgs& a, bool noalloc) {
@@ -201,15 +214,26 @@ int run_linear(const mq::LinearArgs& a, hipStream_t s, bool noalloc = false) {
     // no-allocation entry point keeps one workgroup per tile
     auto gemmw = [&]() -> hipError_t {
       const int cus = num_cus_current();
-      const bool split = !noalloc && g_gemm_split.load() != 0;
+      bool split = !noalloc && g_gemm_split.load() != 0;
       void* ws = nullptr;
-      const size_t need = split ? mq::gemmw_ws_bytes(a, cus, true) : 0;
+      size_t need = split ? mq::gemmw_ws_bytes(a, cus, true) : 0;
       hipError_t we = workspace_for(s, need, &ws);
+      if (we == hipErrorStreamCaptureUnsupported) {
+        // under capture with a workspace too small for this shape: one
+        // workgroup per tile (no workspace) rather than an error
+        split = false;
+        need = 0;
+        ws = nullptr;
+        we = hipSuccess;
+      }
       if (we != hipSuccess) return we;
       path = need ? PATH_GEMMW_SPLIT : PATH_GEMMW;
       return mq::gemmw_launch(a, cus, ws, s, split);
     };
-    if (impl == 0 && mq::gemmw_supported(a, num_cus_current())) {
+    if ((impl == 0 && gemm16_auto(a)) || (impl == 2 && mq::gemm16_supported(a))) {
+      e = mq::gemm16_launch(a, s, nullptr);
+      path = PATH_GEMM16;
+    } else if ((impl == 0 || impl == 2) && mq::gemmw_supported(a, num_cus_current())) {
       e = gemmw();
     } else if (mq::tiled_supported(a)) {
       e = mq::tiled_launch(a, s);
@@ -578,7 +602,8 @@ MQ_API int mq_set_option(const char* key, int64_t value) {
     return MQ_SUCCESS;
   }
   if (std::strcmp(key, "gemm_impl") == 0) {
-    if (value != 0 && value != 1) return fail(MQ_INVALID_ARGUMENT, "set_option: gemm_impl must be 0 or 1");
+    if (value != 0 && value != 1 && value != 2)
+      return fail(MQ_INVALID_ARGUMENT, "set_option: gemm_impl must be 0, 1 or 2");
     g_gemm_impl.store((int)value);
     return MQ_SUCCESS;
   }

@@ -14,6 +14,14 @@
 #pragma once
 #pragma clang fp contract(off)
 
+// gfx950 only: the cross-workgroup handoffs (split-K GEMV, K-split GEMM,
+// row-block K parts, argmax) publish with relaxed system-scope atomics and
+// s_waitcnt, an ordering argument made for gfx950's lowering of the memory
+// model; the inline-asm MFMA code assumes gfx950's operand layouts.
+#if defined(__HIP_DEVICE_COMPILE__) && !defined(__gfx950__)
+#error "the metal-native_amd kernels are written for gfx950 only"
+#endif
+
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 

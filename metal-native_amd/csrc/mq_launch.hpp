@@ -105,6 +105,12 @@ bool gemmw_supported(const LinearArgs& a, int num_cus);
 size_t gemmw_ws_bytes(const LinearArgs& a, int num_cus, bool allow_split);
 hipError_t gemmw_launch(const LinearArgs& a, int num_cus, void* ws, hipStream_t s, bool allow_split);
 
+// 128-row int4 GEMM (16x16x32 MFMA, one workgroup per 128 x 80 tile, no
+// workspace).  trace: optional per-wave timestamps (null in the library).
+bool gemm16_supported(const LinearArgs& a);
+int gemm16_workgroups(const LinearArgs& a);
+hipError_t gemm16_launch(const LinearArgs& a, hipStream_t s, uint64_t* trace);
+
 // 16x16x32 MFMA GEMM, K steps of 32 (fallback for shapes the GEMM above does not take).
 bool tiled_supported(const LinearArgs& a);
 hipError_t tiled_launch(const LinearArgs& a, hipStream_t s);

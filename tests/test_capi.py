@@ -84,7 +84,8 @@ def test_set_option(lib):
     assert lib.mq_set_option(b"gemv_tiles_per_wg", 3) == 4
     assert lib.mq_set_option(b"nonsense", 1) == 4
     assert b"unknown key" in lib.mq_last_error()
-    assert lib.mq_set_option(b"gemm_impl", 2) == 4
+    assert lib.mq_set_option(b"gemm_impl", 3) == 4
+    assert lib.mq_set_option(b"gemm_impl", 2) == 0
     assert lib.mq_set_option(b"gemm_impl", 0) == 0
     assert lib.mq_set_option(b"force_path", 0) == 0
 

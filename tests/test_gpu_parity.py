@@ -27,8 +27,9 @@ GOLD = os.path.join(os.path.dirname(__file__), "golden", "known_answers.npz")
 
 PATHS = {"tiled": 2, "generic": 3, "decode": 6, "rows": 7}
 # force_path "tiled" selects the prefill GEMM family; the kernel that ran is
-# reported as "gemmw" (register-operand GEMM) or "tiled" (16x16x32 fallback)
-FAMILY = {"gemmw": "tiled", "gemmw_split": "tiled"}
+# reported as "gemm16" (128-row int4 GEMM), "gemmw" (register-operand GEMM) or
+# "tiled" (16x16x32 fallback)
+FAMILY = {"gemmw": "tiled", "gemmw_split": "tiled", "gemm16": "tiled"}
 
 
 @pytest.fixture(scope="module")
@@ -277,8 +278,17 @@ def test_config3_llama3b_qkv_prefill(mn, gpu):
     x, wp, s, z = O.make_int4_problem(M, K, N, g, seed=0)
     ref = O.matmul_f32acc(x, O.dequant_int4(wp, s, z, K, g))
     y, taken = run_dm(mn, gpu, x, wp, s, z, g, "int4")
-    assert taken == "gemmw"
+    assert taken == "gemm16"
     check_close(y, ref, "config3")
+    for impl, want in ((1, "tiled"), (2, "gemm16")):
+        mn.set_option("gemm_impl", impl)
+        try:
+            y2, _ = run_dm(mn, gpu, x, wp, s, z, g, "int4", "tiled")
+            ran = mn.last_path()
+        finally:
+            mn.set_option("gemm_impl", 0)
+        assert ran == want, ran
+        check_close(y2, ref, f"config3 [{ran}]")
 
 
 @pytest.mark.parametrize("M", [1, 16, 64])
@@ -489,6 +499,42 @@ def test_hip_graph_replay(mn, gpu):
         np.testing.assert_array_equal(out.cpu().numpy().view(np.uint16), eager.view(np.uint16),
                                       err_msg=f"replay {rep}")
         _ = host(mn.dequant_matmul(xa[:1].contiguous(), wa, sa, za, 128, "int4"))  # eager work between
+
+
+def test_graph_survives_workspace_growth(mn, gpu):
+    """A graph captured on a stream keeps the address of that stream's
+    split-K workspace; a later, larger shape on the same stream grows the
+    workspace, and the graph must still replay correctly (the superseded
+    buffer is kept, not freed)."""
+    say("graph across workspace growth")
+    x, wp, s, z = O.make_int4_problem(8, 2048, 512, 64, seed=4)
+    xa, wa, sa, za = (dev(v, gpu) for v in (x, wp, s, z))
+    xb, wb, sb, zb = (dev(v, gpu) for v in O.make_int4_problem(16, 18944, 3584, 128, seed=5))
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    mn.set_option("force_path", PATHS["decode"])
+    try:
+        with torch.cuda.stream(stream):
+            eager = mn.dequant_matmul(xa, wa, sa, za, 64, "int4")  # allocates this stream's workspace
+        torch.cuda.current_stream().wait_stream(stream)
+        eager = host(eager)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            out = mn.dequant_matmul(xa, wa, sa, za, 64, "int4")
+        with torch.cuda.stream(stream):
+            big = mn.dequant_matmul(xb, wb, sb, zb, 128, "int4")  # needs a larger workspace
+        torch.cuda.synchronize()
+        assert mn.last_path() == "decode"
+        for rep in range(3):
+            with torch.cuda.stream(stream):
+                torch.empty(64 << 20, dtype=torch.uint8, device=gpu).fill_(0xFF)   # reuse of freed memory shows
+                graph.replay()
+            torch.cuda.synchronize()
+            np.testing.assert_array_equal(out.cpu().numpy().view(np.uint16), eager.view(np.uint16),
+                                          err_msg=f"replay {rep}")
+        del big
+    finally:
+        mn.set_option("force_path", 0)
 
 
 def test_errors_on_gpu_tensors(mn, gpu):
@@ -828,6 +874,8 @@ def test_prefill_gemm_split_k(mn, gpu, qt, g, epi, M, K, N):
     ("tiled", 64, 1216, 256, 64, "int8", 0),
     ("tiled", 64, 3104, 256, 32, "int4", 1),       # the 16x16x32 tiled GEMM
     ("tiled", 40, 1216, 256, 64, "int8", 1),
+    ("tiled", 64, 1024, 256, 32, "int4", 2),       # the 128-row int4 GEMM
+    ("tiled", 130, 2048, 200, 128, "int4", 2),
     ("generic", 3, 1000, 100, 128, "int4", 0),
 ])
 def test_weight_rows_do_not_see_other_rows_scales(mn, gpu, path, M, K, N, g, qt, impl):
@@ -876,7 +924,7 @@ ONEHOT_ZEROS = np.array([0x0000, 0x8000, 0x0001, 0x3C00, 0xBC00, 0x2E66, 0x4A00]
 
 @pytest.mark.parametrize("qt", ["int4", "int8"])
 @pytest.mark.parametrize("path,impl,M", [("rows", 0, 8), ("decode", 0, 8), ("generic", 0, 8), ("tiled", 0, 64),
-                                         ("tiled", 1, 64)])
+                                         ("tiled", 1, 64), ("tiled", 2, 64)])
 def test_one_hot_selects_dequantized_weights(mn, gpu, qt, path, impl, M):
     """One-hot activation rows make every output the fp32 sum of one product
     w * 1 and zeros, i.e. the dequantized weight itself: each kernel's
@@ -910,5 +958,93 @@ def test_one_hot_selects_dequantized_weights(mn, gpu, qt, path, impl, M):
             bad = y != ref                                   # -0 == +0
             assert not bad.any(), (f"{qt} {path} impl={impl}: {bad.sum()} outputs differ from the dequantized "
                                    f"weights, e.g. {y[bad][:4]} vs {ref[bad][:4]}")
+    finally:
+        mn.set_option("gemm_impl", 0)
+
+
+# ---------------------------------------------------------------------------
+# the 128-row int4 prefill GEMM (gemm16)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("M,K,N,g,epi", [
+    (512, 3072, 5120, 64, None),        # config 3 at g = 64 and g = 32 (benched)
+    (512, 3072, 5120, 32, "bias"),
+    (200, 1024, 1000, 32, None),        # ragged M and N (80-column tiles)
+    (130, 2048, 400, 64, "bias_relu"),
+    (256, 1024, 240, 1024, "bias_silu"),  # one group per row (per-channel scales)
+    (300, 1536, 480, 128, "residual"),
+    (96, 4096, 88, 128, None),          # a K-tile count per wave that is odd, N % 8 != 0
+    (1, 512, 160, 128, None),
+])
+def test_gemm16(mn, gpu, M, K, N, g, epi):
+    """The 128-row int4 GEMM forced on ragged, grouped and per-channel
+    shapes with every element-wise epilogue: within the bound of the
+    oracle's fp32-accumulated result, and bit-identical on a second run
+    (the four partial tiles of a workgroup are summed in a fixed order)."""
+    say(f"gemm16 M={M} K={K} N={N} g={g} {epi}")
+    x, wp, s, z = O.make_int4_problem(M, K, N, g, seed=M + K + N + g)
+    acc = O.matmul_f32acc(x, O.dequant_int4(wp, s, z, K, g))
+    kw, b, res = {}, None, None
+    if epi in ("bias", "bias_relu", "bias_silu"):
+        b = np.random.default_rng(N).standard_normal(N).astype(np.float16)
+        kw = {"epilogue": epi, "bias": dev(b, gpu)}
+    elif epi == "residual":
+        res = np.random.default_rng(M).standard_normal((M, N)).astype(np.float16)
+        kw = {"epilogue": "residual", "residual": dev(res, gpu)}
+    mn.set_option("gemm_impl", 2)
+    try:
+        y, _ = run_dm(mn, gpu, x, wp, s, z, g, "int4", "tiled", **kw)
+        ran = mn.last_path()
+        y2, _ = run_dm(mn, gpu, x, wp, s, z, g, "int4", "tiled", **kw)
+    finally:
+        mn.set_option("gemm_impl", 0)
+    assert ran == "gemm16", ran
+    if epi is None:
+        check_close(y, acc, "gemm16")
+    else:
+        check_epilogue(y, acc, epi, f"gemm16 {epi}", bias=b, residual=res)
+    np.testing.assert_array_equal(y2.view(np.uint16), y.view(np.uint16))
+
+
+def test_gemm16_strided_output_and_inplace_residual(mn, gpu):
+    """An output whose rows are not 16-byte aligned (element stride N+1) takes
+    the element-wise store path; an in-place residual reads every element
+    before the workgroup that owns it stores it."""
+    M, K, N, g = 256, 1024, 320, 64
+    x, wp, s, z = O.make_int4_problem(M, K, N, g, seed=5)
+    acc = O.matmul_f32acc(x, O.dequant_int4(wp, s, z, K, g))
+    res = np.random.default_rng(6).standard_normal((M, N)).astype(np.float16)
+    mn.set_option("gemm_impl", 2)
+    try:
+        big = torch.zeros((M, N + 1), dtype=torch.float16, device=gpu)
+        out = big[:, :N]
+        out.copy_(dev(res, gpu))
+        mn.set_option("force_path", PATHS["tiled"])
+        mn.dequant_matmul(dev(x, gpu), dev(wp, gpu), dev(s, gpu), dev(z, gpu), g, "int4",
+                          epilogue="residual", residual=out, out=out)
+        ran = mn.last_path()
+        y = host(out)
+        rest = host(big[:, N])
+    finally:
+        mn.set_option("force_path", 0)
+        mn.set_option("gemm_impl", 0)
+    assert ran == "gemm16", ran
+    check_epilogue(y, acc, "residual", "gemm16 strided in place", residual=res)
+    assert (rest == 0).all(), "a store reached past the output's columns"
+
+
+def test_gemm16_unsupported_shapes_fall_back(mn, gpu):
+    """K % 64 != 0 and int8 weights are not taken by the 128-row GEMM even
+    when it is forced: the prefill family's other kernels run them."""
+    mn.set_option("gemm_impl", 2)
+    try:
+        x, wp, s, z = O.make_int4_problem(128, 3104, 256, 32, seed=1)
+        y, _ = run_dm(mn, gpu, x, wp, s, z, 32, "int4", "tiled")
+        assert mn.last_path() in ("gemmw", "gemmw_split", "tiled"), mn.last_path()
+        check_close(y, O.matmul_f32acc(x, O.dequant_int4(wp, s, z, 3104, 32)), "gemm16 fallback int4")
+        x, q, s8, z8, g8 = O.make_int8_problem(128, 1024, 256, seed=2)
+        y, _ = run_dm(mn, gpu, x, q, s8, z8, g8, "int8", "tiled")
+        assert mn.last_path() in ("gemmw", "gemmw_split", "tiled"), mn.last_path()
+        check_close(y, O.matmul_f32acc(x, O.dequant_int8(q, s8, z8, 1024, g8)), "gemm16 fallback int8")
     finally:
         mn.set_option("gemm_impl", 0)
