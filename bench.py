@@ -188,6 +188,60 @@ def measure(name, steps, warmup, device):
     return res
 
 
+def read_ceiling(name, steps, warmup, device):
+    """The one-launch read ceiling of the headline's bytes: mq_read_probe over
+    as many rotated copies of the config's algorithmic bytes as the headline
+    rotates, timed exactly like the headline (graph replay, HIP events)."""
+    import ctypes
+
+    import torch
+
+    from metal_native import _lib
+
+    qtype, M, K, N, g, epi, bound = CONFIGS[name]
+    per_copy = algo_bytes(qtype, M, K, N, g, epi)
+    copies = max(2, min(256, -(-ROTATE_TARGET // per_copy)))
+    bufs = [torch.randint(0, 256, (per_copy,), dtype=torch.uint8, device=device) for _ in range(copies)]
+    sink = torch.zeros(int(_lib.lib.mq_read_probe_sink_size()) // 4 + 1, dtype=torch.int32, device=device)
+    stream = torch.cuda.Stream(device)
+    stream.wait_stream(torch.cuda.current_stream(device))
+
+    def fn(i):
+        rc = _lib.lib.mq_read_probe(ctypes.c_void_p(bufs[i % copies].data_ptr()), per_copy,
+                                    ctypes.c_void_p(sink.data_ptr()), ctypes.c_void_p(stream.cuda_stream))
+        if rc != 0:
+            raise RuntimeError(_lib.lib.mq_last_error().decode())
+
+    with torch.cuda.stream(stream):
+        for i in range(copies):
+            fn(i)
+    torch.cuda.synchronize(device)
+    gwarm = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gwarm, stream=stream):
+        for i in range(max(1, warmup)):
+            fn(i)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for i in range(steps):
+            fn(i)
+    cur = torch.cuda.current_stream(device)
+    gwarm.replay()
+    torch.cuda.synchronize(device)
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record(cur)
+    graph.replay()
+    t1.record(cur)
+    torch.cuda.synchronize(device)
+    us = t0.elapsed_time(t1) * 1000.0 / steps
+    gbs = per_copy / (us * 1e-6) / 1e9
+    del graph, gwarm, bufs
+    torch.cuda.empty_cache()
+    return {"us_per_launch": round(us, 3), "GB/s": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+            "bytes_per_launch": per_copy, "copies_rotated": copies,
+            "what": "mq_read_probe: one read of the headline's algorithmic bytes per launch, no compute"}
+
+
 def decode_bench(device):
     """28-layer Qwen2.5-7B-shaped decoder, int4 g128
     everywhere (lm_head included), batch 1, 512-token random KV cache, greedy
@@ -418,6 +472,13 @@ def main():
         results[n] = measure(n, steps, args.warmup, device)
         log(f"[bench] {n}: {json.dumps(results[n])}")
     head = results[HEADLINE]
+    try:
+        ceil = read_ceiling(HEADLINE, max(200, args.steps // 4), args.warmup, device)
+        results["read_ceiling_cfg2"] = ceil
+        log(f"[bench] read ceiling: {json.dumps(ceil)}")
+    except Exception as e:  # noqa: BLE001  (the headline line must still print)
+        ceil = None
+        results["read_ceiling_cfg2"] = {"error": repr(e)}
 
     if not args.only_headline and not args.only:
         try:
@@ -470,6 +531,8 @@ def main():
         "cpu_baseline": cpu,
         "extra": results,
     }
+    if ceil:
+        line["headline_frac_of_read_ceiling"] = round(head["GB/s"] / ceil["GB/s"], 4)
     prefill = results.get("cfg3_llama3b_qkv_m512")
     if prefill:
         line["prefill_TFLOP/s"] = prefill["TFLOP/s"]

@@ -223,6 +223,16 @@ MQ_API int mq_argmax_embed_f16(const void* logits, int64_t vocab, const void* em
                                int64_t* token, int64_t* pos, void* x, void* workspace, int64_t workspace_bytes,
                                void* stream);
 
+/* Read probe: a measurement aid with no reference counterpart.  Reads the
+ * `bytes` (< 2^31) bytes at p once, in one launch, the fastest way found on
+ * gfx950 (one 12-wave workgroup per CU, 4-deep rings of 16-byte
+ * non-temporal loads), and writes nothing but an occasional flag into sink
+ * (mq_read_probe_sink_size() bytes).  The time of one launch bounds what any
+ * kernel that reads the same bytes in one launch can reach; bench.py reports
+ * it beside the headline. */
+MQ_API int64_t mq_read_probe_sink_size(void);
+MQ_API int mq_read_probe(const void* p, int64_t bytes, void* sink, void* stream);
+
 /* Kernel-path override and layout knobs for tests and tuning (no reference
  * counterpart).  Keys: "force_path" (0 automatic, 2 the prefill GEMM family,
  * 3 generic, 6 split-K decode GEMV, 7 row-block decode GEMV), "gemv_steps"

@@ -592,6 +592,16 @@ MQ_API int mq_argmax_embed_f16(const void* logits, int64_t vocab, const void* em
   return MQ_SUCCESS;
 }
 
+MQ_API int64_t mq_read_probe_sink_size(void) { return (int64_t)12 * num_cus_current() * 4; }
+
+MQ_API int mq_read_probe(const void* p, int64_t bytes, void* sink, void* stream) {
+  if (!p || !sink) return fail(MQ_INVALID_ARGUMENT, "read_probe: null pointer argument");
+  if (bytes < 1 || bytes >= ((int64_t)1 << 31)) return fail(MQ_INVALID_ARGUMENT, "read_probe: bytes must be in [1, 2^31)");
+  hipError_t e = mq::read_probe_launch(p, bytes, sink, num_cus_current(), (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "read_probe: kernel launch failed");
+  return MQ_SUCCESS;
+}
+
 MQ_API int mq_set_option(const char* key, int64_t value) {
   if (!key) return fail(MQ_INVALID_ARGUMENT, "set_option: null key");
   if (std::strcmp(key, "force_path") == 0) {

@@ -295,8 +295,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   // zero scales
   static_assert(WPF % 2 == 0, "slot parity");
   int t = kt0;
+  uint64_t Tf = 0;
   do {
     tile(std::integral_constant<int, 0>{}, slot0, slot1, t);
+    if (t == kt0) Tf = __builtin_amdgcn_s_memrealtime();
     tile(std::integral_constant<int, 1>{}, slot1, slot0, t + 1);
     if (WPF > 2) {
       tile(std::integral_constant<int, 2 % WPF>{}, slot0, slot1, t + 2);
@@ -393,7 +395,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   }
   if (p.trace != nullptr && lane == 0) {
     uint64_t* o = p.trace + ((size_t)blockIdx.x * 4 + w) * 8;
-    o[0] = T0; o[1] = T1; o[2] = T2; o[3] = T3; o[4] = T4; o[5] = T5; o[6] = __builtin_amdgcn_s_memrealtime(); o[7] = 0;
+    o[0] = T0; o[1] = T1; o[2] = T2; o[3] = T3; o[4] = T4; o[5] = T5; o[6] = __builtin_amdgcn_s_memrealtime(); o[7] = Tf;
   }
 }
 

@@ -161,6 +161,8 @@ hipError_t argmax_embed_launch(const void* logits, int64_t V, const void* embed,
                                int64_t* pos, void* x, void* ws, hipStream_t s);
 
 hipError_t swiglu_launch(const void* gate, const void* up, void* out, int64_t n, hipStream_t s);
+// One-launch read of `bytes` bytes (measurement aid); sink: 12 * num_cus u32.
+hipError_t read_probe_launch(const void* p, int64_t bytes, void* sink, int num_cus, hipStream_t s);
 
 // fp16 GEMV with B stored [K, N] (transpose_b == false): C = A . B.
 hipError_t vecmat_kn_launch(const void* A, int64_t lda, const void* B, int64_t ldb,

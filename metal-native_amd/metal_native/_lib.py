@@ -40,6 +40,8 @@ _i32 = ctypes.c_int32
 
 # name -> (restype, argtypes)
 SIGNATURES = {
+    "mq_read_probe_sink_size": (_i64, []),
+    "mq_read_probe": (_i32, [_c_void_p, _i64, _c_void_p, _c_void_p]),
     "mq_dequant_matmul": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p,
                                  _i64, _i64, _i64, _i64, _i32, _i32, _i32, _c_void_p, _c_void_p, _i64,
                                  _c_void_p]),

@@ -5,8 +5,9 @@ g128 everywhere, 512-token cache).
 * Every linear of every layer (113 of them) runs through the library's
   decode path on the fp32 reference chain's own fp16 input and is checked
   against the fp32-accumulated product with weights from ``mn.dequantize``
-  (bit-exact to the reference formula, pinned by the parity tests), at the
-  contract tolerance |y - y_ref| <= 1e-2 + 1e-3 |y_ref|.
+  (bit-exact to the reference formula, pinned by the parity tests; 64
+  random rows of every layer are also compared with the CPU oracle's
+  dequant here), at the contract tolerance |y - y_ref| <= 1e-2 + 1e-3 |y_ref|.
 * One fused decode step (norms inside the GEMVs, fused attention) agrees
   with the fp32 reference step on the logits at the same contract
   tolerance (measured on one MI355X: max error 4.9e-4, under 5 % of the
@@ -32,10 +33,27 @@ def model(gpu):
     torch.cuda.empty_cache()
 
 
-def deq(ql):
-    import metal_native as mn
+def deq(ql, spot_rows=64):
+    """The reference chain's weights: ``mn.dequantize`` of the layer, with
+    ``spot_rows`` random rows of it checked bit-exact against the CPU
+    oracle's two-rounding dequant, so the chain does not rest on the
+    library's dequantize alone."""
+    import numpy as np
 
-    return mn.dequantize(ql.wp, ql.scales, ql.zeros, ql.g, "int4")
+    import metal_native as mn
+    from oracle import mq_oracle as O
+
+    w = mn.dequantize(ql.wp, ql.scales, ql.zeros, ql.g, "int4")
+    if spot_rows:
+        N = w.shape[0]
+        K = w.shape[1]
+        rows = np.random.default_rng(N + K).choice(N, size=min(spot_rows, N), replace=False)
+        idx = torch.from_numpy(rows).to(w.device)
+        want = O.dequant_int4(ql.wp.index_select(0, idx).cpu().numpy(), ql.scales.index_select(0, idx).cpu().numpy(),
+                              ql.zeros.index_select(0, idx).cpu().numpy(), K, ql.g)
+        got = w.index_select(0, idx).cpu().numpy()
+        assert np.array_equal(got.view(np.uint16), want.view(np.uint16)), f"dequantize rows {rows[:4]}.. differ"
+    return w
 
 
 def test_every_linear_at_config5(model, gpu):
