@@ -158,13 +158,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const uint32_t so = past ? 0u : (uint32_t)t * 128u;
     dma16(past ? nullr : ar, slot + 64 * i, adma, so + i * rstride);
   };
-  // prologue loads: activations of the first two K-tiles, weights of the first WPF
+  // prologue loads: what the first K-tile's k-step 0 needs (its
+  // activations and weights) and the next K-tile's weights; the rest of
+  // the pipeline's loads go out when the first K-tile starts (a deep burst
+  // issued here would hold back the first data: every CU starts at once)
 #pragma unroll
   for (int i = 0; i < 16; ++i) dma_one(kt0, slot0, i);
-#pragma unroll
-  for (int d = 0; d < WPF; ++d) load_w(kt0 + d, wring[d]);
-#pragma unroll
-  for (int i = 0; i < 16; ++i) dma_one(kt0 + 1, slot1, i);
+  load_w(kt0, wring[0]);
+  load_w(kt0 + 1, wring[1]);
   // scale | zero table writes (s | z << 16 per entry)
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
@@ -219,7 +220,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       const uint32_t d = nstep ? nwt[j].y : nwt[j].x;
       const uint32_t e = nsz[j];
       uint32_t x0, x1, x2, x3;
-#define MF(i) asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+a"(acc[i][j]) : "v"(af[i]), "v"(bq[j]))
+#define MF(i) asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+a"(acc[i][j]) : "v"(bq[j]), "v"(af[i]))
 #define PERM(x, sel) asm volatile("v_perm_b32 %0, 0, %1, %2" : "=v"(x) : "v"(d), "s"(sel))
 #define ANDOR(x) asm volatile("v_and_or_b32 %0, %0, %1, %2" : "+v"(x) : "v"(nmask), "s"(magic))
 #define FMA(x) asm volatile("v_pk_fma_f16 %0, %0, %1, %2" : "+v"(x) : "s"(fm), "v"(fo))
@@ -275,6 +276,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   auto tile = [&](auto rc, u4* cur, u4* nxt, int t) {
     constexpr int R = decltype(rc)::value;
     constexpr int R1 = (R + 1) % WPF;
+    if (R == 0 && t == kt0) {   // the first K-tile: the rest of the prologue
+#pragma unroll
+      for (int i = 0; i < 16; ++i) dma_one(kt0 + 1, slot1, i);
+#pragma unroll
+      for (int d = 2; d < WPF; ++d) load_w(kt0 + d, wring[d]);
+    }
     read_sz(t + 1, sz2);
     // k-step 0 of tile t; prepares k-step 1; then refills the weight slot
     step(afA, bqA, cur, 1, afB, wring[R], sz, 1, bqB, [&](int) {});
@@ -309,34 +316,43 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   const uint64_t T2 = __builtin_amdgcn_s_memrealtime();
 
   // ---- the four partial tiles meet in LDS ----
+  // Block b = i*NB + j is owned by wave b % 4.  Each wave writes its
+  // partials of the blocks it does not own into its own activation slots
+  // (free once its K loop is done: no barrier before), 1 KiB per block in
+  // block order, 16 bytes per lane (conflict-free); after one barrier each
+  // owner sums the four partials of its blocks in wave order
+  // (deterministic).
   asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");   // MFMA results retired
 #pragma unroll
   for (int i = 0; i < MBK; ++i)
 #pragma unroll
     for (int j = 0; j < NB; ++j) asm volatile("" : "+a"(acc[i][j]));
-  __syncthreads();   // every wave is done with its activation slots and the table
-  const uint64_t T3 = __builtin_amdgcn_s_memrealtime();
-  // block b = i*NB + j is owned by wave b % 4; the others write slot
-  // (b, rank) of 1 KiB (16 bytes per lane, conflict-free)
-  auto rslot = [&](int k) -> f4* {
-    return k < 64 ? (f4*)&lds_a0[0][0] + k * 64 : (f4*)&lds_a1[0][0] + (k - 64) * 64;
+  // slot of block b in wave ww's region (its blocks not owned by ww, in order)
+  auto rslot = [&](int ww, int b) -> f4* {
+    const int idx = b - (b > ww ? (b - ww + 3) / 4 : 0);
+    return idx < 16 ? (f4*)&lds_a0[ww][0] + idx * 64 : (f4*)&lds_a1[ww][0] + (idx - 16) * 64;
   };
-  // fp32 sums staged as [128][RS] in the first activation array
-  constexpr int RS = BN + 4;
-  float* res = (float*)&lds_a0[0][0];
-  static_assert(128 * RS * 4 <= 4 * 1024 * 16, "result tile fits the first activation array");
+  static_assert(MBK * NB - (MBK * NB) / 4 <= 32, "a wave's partials fit in its two activation slots");
   constexpr int NOWN = (MBK * NB + 3) / 4;
   f4 own[NOWN];
+  uint64_t Tb = 0;
   auto gather = [&](auto wc) {
     constexpr int W = decltype(wc)::value;
+    // straight from the accumulator registers (no copies through VGPRs);
+    // the 24 wait states above cover the MFMA-to-LDS-read dependency
 #pragma unroll
     for (int i = 0; i < MBK; ++i)
 #pragma unroll
       for (int j = 0; j < NB; ++j) {
-        const int b = i * NB + j, ow = b & 3;
-        if (ow != W) rslot(b * 3 + (W < ow ? W : W - 1))[lane] = acc[i][j];
+        const int b = i * NB + j;
+        if ((b & 3) != W) {
+          const uint32_t la = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) f4*)(rslot(W, b) + lane);
+          asm volatile("ds_write_b128 %0, %1" :: "v"(la), "a"(acc[i][j]) : "memory");
+        }
       }
-    __syncthreads();
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __syncthreads();   // every wave's partials are in LDS
+    Tb = __builtin_amdgcn_s_memrealtime();
 #pragma unroll
     for (int i = 0; i < MBK; ++i)
 #pragma unroll
@@ -347,55 +363,95 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
         for (int ww = 0; ww < 4; ++ww) {   // wave order: deterministic
           if (ww == W) sum += acc[i][j];
-          else sum += rslot(b * 3 + (ww < W ? ww : ww - 1))[lane];
+          else sum += rslot(ww, b)[lane];
         }
         own[b >> 2] = sum;
       }
   };
+  const uint64_t T3 = __builtin_amdgcn_s_memrealtime();
   if (w == 0) gather(std::integral_constant<int, 0>{});
   else if (w == 1) gather(std::integral_constant<int, 1>{});
   else if (w == 2) gather(std::integral_constant<int, 2>{});
   else gather(std::integral_constant<int, 3>{});
   __syncthreads();   // every partial has been read
   const uint64_t T4 = __builtin_amdgcn_s_memrealtime();
-  // owned block b = 4u + w: rows 16i + 4q + v, column 16j + c
-#pragma unroll
-  for (int u = 0; u < NOWN; ++u) {
-    const int b = 4 * u + w;
-    if (b >= MBK * NB) break;
-    const int i = b / NB, j = b - i * NB;
-#pragma unroll
-    for (int v = 0; v < 4; ++v) res[(16 * i + 4 * q + v) * RS + 16 * j + c] = own[u][v];
-  }
-  __syncthreads();
-  const uint64_t T5 = __builtin_amdgcn_s_memrealtime();
-  // ---- epilogue on the fp32 sums, fp16 rounding, 16-byte stores: 8
-  // columns of one row per thread and piece ----
-  constexpr int PPR = BN / 8;   // pieces per row
+  constexpr int PPR = BN / 8;              // 16-byte pieces per output row
+  constexpr int NPC = 128 * PPR / 256;      // pieces per thread
+  static_assert(128 * PPR % 256 == 0, "whole pieces per thread");
   const int kind = p.ep.epi;
-  for (int pc = tid; pc < 128 * PPR; pc += 256) {
-    const int r = pc / PPR, cc = 8 * (pc - r * PPR);
-    const int row = m0 + r, col = n0 + cc;
-    if (row >= p.M || col >= p.N) continue;
-    const f4 v0 = *(const f4*)&res[r * RS + cc], v1 = *(const f4*)&res[r * RS + cc + 4];
-    float v[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-    const int ncol = min(8, p.N - col);
-    if (kind != EPI_NONE) {
-      for (int e = 0; e < ncol; ++e) v[e] = epi_apply(v[e], (int64_t)row, col + e, p.ep);
-    }
-    _Float16* dst = p.C + (int64_t)row * p.ldc + col;
-    if (p.vec_store && ncol == 8) {
-      h8 hv;
+  if (kind == EPI_NONE && p.vec_store && m0 + 128 <= p.M && n0 + BN <= p.N) {
+    // fp16 results staged as [128][SS] halves (rows 16 bytes apart mod 128
+    // bytes: the 16 rows of one store group fall in different banks), then
+    // 16-byte stores, every LDS read of a thread issued before its stores
+    constexpr int SS = BN + 8;
+    _Float16* stg = (_Float16*)&lds_a0[0][0];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) hv[e] = (_Float16)v[e];
-      *(h8*)dst = hv;
-    } else {
-      for (int e = 0; e < ncol; ++e) dst[e] = (_Float16)v[e];
+    for (int u = 0; u < NOWN; ++u) {
+      const int b = 4 * u + w;
+      if (b >= MBK * NB) break;
+      const int i = b / NB, j = b - i * NB;
+      typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+      *(h4*)&stg[(16 * i + c) * SS + 16 * j + 4 * q] =
+          (h4){(_Float16)own[u][0], (_Float16)own[u][1], (_Float16)own[u][2], (_Float16)own[u][3]};
+    }
+    __syncthreads();
+    const uint64_t T5 = __builtin_amdgcn_s_memrealtime();
+    h8 pv[NPC];
+#pragma unroll
+    for (int e = 0; e < NPC; ++e) {
+      const int pc = tid + 256 * e;
+      const int r = pc / PPR, cc = 8 * (pc - r * PPR);
+      pv[e] = *(const h8*)&stg[r * SS + cc];
+    }
+#pragma unroll
+    for (int e = 0; e < NPC; ++e) {
+      const int pc = tid + 256 * e;
+      const int r = pc / PPR, cc = 8 * (pc - r * PPR);
+      *(h8*)(p.C + (int64_t)(m0 + r) * p.ldc + n0 + cc) = pv[e];
+    }
+    if (p.trace != nullptr && lane == 0) {
+      uint64_t* o = p.trace + ((size_t)blockIdx.x * 4 + w) * 8;
+      o[5] = T5;
+    }
+  } else {
+    // fp32 sums staged as [128][RS]; the epilogue is applied per element,
+    // then fp16 rounding and 16-byte stores where the rows allow
+    constexpr int RS = BN + 4;
+    float* res = (float*)&lds_a0[0][0];
+    static_assert(128 * RS * 4 <= 4 * 1024 * 16, "result tile fits the first activation array");
+    // owned block b = 4u + w: row 16i + c, columns 16j + 4q .. +3
+#pragma unroll
+    for (int u = 0; u < NOWN; ++u) {
+      const int b = 4 * u + w;
+      if (b >= MBK * NB) break;
+      const int i = b / NB, j = b - i * NB;
+      *(f4*)&res[(16 * i + c) * RS + 16 * j + 4 * q] = own[u];
+    }
+    __syncthreads();
+    for (int pc = tid; pc < 128 * PPR; pc += 256) {
+      const int r = pc / PPR, cc = 8 * (pc - r * PPR);
+      const int row = m0 + r, col = n0 + cc;
+      if (row >= p.M || col >= p.N) continue;
+      const f4 v0 = *(const f4*)&res[r * RS + cc], v1 = *(const f4*)&res[r * RS + cc + 4];
+      float v[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+      const int ncol = min(8, p.N - col);
+      if (kind != EPI_NONE) {
+        for (int e = 0; e < ncol; ++e) v[e] = epi_apply(v[e], (int64_t)row, col + e, p.ep);
+      }
+      _Float16* dst = p.C + (int64_t)row * p.ldc + col;
+      if (p.vec_store && ncol == 8) {
+        h8 hv;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) hv[e] = (_Float16)v[e];
+        *(h8*)dst = hv;
+      } else {
+        for (int e = 0; e < ncol; ++e) dst[e] = (_Float16)v[e];
+      }
     }
   }
   if (p.trace != nullptr && lane == 0) {
     uint64_t* o = p.trace + ((size_t)blockIdx.x * 4 + w) * 8;
-    o[0] = T0; o[1] = T1; o[2] = T2; o[3] = T3; o[4] = T4; o[5] = T5; o[6] = __builtin_amdgcn_s_memrealtime(); o[7] = Tf;
+    o[0] = T0; o[1] = T1; o[2] = T2; o[4] = T4; o[6] = __builtin_amdgcn_s_memrealtime(); o[7] = Tf; o[3] = Tb;
   }
 }
 
