@@ -190,6 +190,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   }
   __syncthreads();
   const uint64_t T1 = __builtin_amdgcn_s_memrealtime();
+  uint64_t Tv = 0;
+  if (p.trace != nullptr) { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); Tv = __builtin_amdgcn_s_memrealtime(); }
 
   // scale|zero of K-tile t for each block; K-tiles past the wave's range
   // get (0, 0), so their (zero) activations meet zero weights
@@ -213,8 +215,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   // of (af[i], bq[j]) one by one, each followed by a share of the 20 VALU
   // ops that dequantize block j of the next k-step, and by a share of the
   // next k-step's fragment reads and of `extra` (refill loads).
-  auto step = [&](const h8 (&af)[MBK], const h8 (&bq)[NB], const u4* nsl, int ns, h8 (&naf)[MBK],
+  // early: all of the next k-step's fragments are read at the start (the
+  // slot they come from can then be refilled during this k-step)
+  auto step = [&](auto earlyc, const h8 (&af)[MBK], const h8 (&bq)[NB], const u4* nsl, int ns, h8 (&naf)[MBK],
                   const u2v (&nwt)[NB], const uint32_t (&nsz)[NB], int nstep, h8 (&nbq)[NB], auto extra) {
+    constexpr bool EARLY = decltype(earlyc)::value;
+    if (EARLY) {
+#pragma unroll
+      for (int i = 0; i < MBK; ++i) naf[i] = __builtin_bit_cast(h8, nsl[ard[ns] + 128 * i]);
+    }
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
       const uint32_t d = nstep ? nwt[j].y : nwt[j].x;
@@ -231,12 +240,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       // RNE(q*s) and RNE(. - z): the reference's two roundings)
       MF(0); PERM(x0, sel0); PERM(x1, sel1); ANDOR(x0); SB();
       MF(1); PERM(x2, sel2); PERM(x3, sel3); ANDOR(x1); SB();
-      if ((j * MBK) / NB < ((j + 1) * MBK) / NB)
+      if (!EARLY && (j * MBK) / NB < ((j + 1) * MBK) / NB)
         naf[(j * MBK) / NB] = __builtin_bit_cast(h8, nsl[ard[ns] + 128 * ((j * MBK) / NB)]);
       SB();
       MF(2); ANDOR(x2); ANDOR(x3); FMA(x0); SB();
       MF(3); FMA(x1); FMA(x2); FMA(x3); SB();
-      if ((j * MBK) / NB + 1 < ((j + 1) * MBK) / NB)
+      if (!EARLY && (j * MBK) / NB + 1 < ((j + 1) * MBK) / NB)
         naf[(j * MBK) / NB + 1] = __builtin_bit_cast(h8, nsl[ard[ns] + 128 * ((j * MBK) / NB + 1)]);
       extra(j);
       SB();
@@ -283,17 +292,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       for (int d = 2; d < WPF; ++d) load_w(kt0 + d, wring[d]);
     }
     read_sz(t + 1, sz2);
-    // k-step 0 of tile t; prepares k-step 1; then refills the weight slot
-    step(afA, bqA, cur, 1, afB, wring[R], sz, 1, bqB, [&](int) {});
-    load_w(t + WPF, wring[R]);
-    // k-step 1 of tile t; the slot is free once k-step 1's fragments are
-    // in registers: refill it (K-tile t+2); prepare tile t+1's k-step 0
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    step(afB, bqB, nxt, 0, afA, wring[R1], sz2, 0, bqA, [&](int j) {
+    // k-step 0 of tile t: reads all of k-step 1's fragments first; once
+    // they are in registers the slot is refilled (K-tile t+2), spread over
+    // the rest of the k-step; then the weight slot is refilled
+    step(std::true_type{}, afA, bqA, cur, 1, afB, wring[R], sz, 1, bqB, [&](int j) {
+      if (j == 0) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
       for (int i = 0; i < 16; ++i)
         if ((i * NB) / 16 == j) dma_one(t + 2, cur, i);
     });
+    load_w(t + WPF, wring[R]);
+    // k-step 1 of tile t; prepares tile t+1's k-step 0 from slot `nxt`
+    step(std::false_type{}, afB, bqB, nxt, 0, afA, wring[R1], sz2, 0, bqA, [&](int) {});
 #pragma unroll
     for (int j = 0; j < NB; ++j) sz[j] = sz2[j];
   };
@@ -451,7 +461,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   }
   if (p.trace != nullptr && lane == 0) {
     uint64_t* o = p.trace + ((size_t)blockIdx.x * 4 + w) * 8;
-    o[0] = T0; o[1] = T1; o[2] = T2; o[4] = T4; o[6] = __builtin_amdgcn_s_memrealtime(); o[7] = Tf; o[3] = Tb;
+    o[0] = T0; o[1] = T1; o[2] = T2; o[4] = T4; o[6] = __builtin_amdgcn_s_memrealtime(); o[7] = Tf; o[3] = Tv;
   }
 }
 
