@@ -238,10 +238,11 @@ MQ_API int mq_read_probe(const void* p, int64_t bytes, void* sink, void* stream)
  * 3 generic, 6 split-K decode GEMV, 7 row-block decode GEMV), "gemv_steps"
  * (K steps per wavefront of the split-K GEMV, 1..8, 0 automatic),
  * "gemv_tiles_per_wg" (row tiles per workgroup: 1, 2 or 4, 0 automatic),
- * "gemm_impl" (prefill GEMM kernel: 0 automatic -- the 128-row int4 GEMM
+ * "gemm_impl" (prefill GEMM kernel: 0 automatic -- the register-dequant
+ * 16x16x32 GEMM (128-row tiles; 64-row tiles for int8 SwiGLU up to M = 64)
  * where its tiles fill the GPU, else the register-operand 32x32x16 kernel
  * where it takes the shape --, 1 always the 16x16x32 tiled kernel, 2 the
- * 128-row int4 GEMM wherever it takes the shape; all compute the same
+ * register-dequant GEMM wherever it takes the shape; all compute the same
  * contract), "gemm_split" (1, the default: the 32x32x16 kernel splits
  * K over several workgroups per output tile where its tiles would leave CUs
  * idle, summing the parts in a fixed order; 0: one workgroup per tile).  A forced path that cannot take the shape falls back
@@ -253,7 +254,7 @@ MQ_API int mq_set_option(const char* key, int64_t value);
  * mq_vecmat_f32 call on this thread launched: 2 16x16x32 tiled GEMM, 3
  * generic, 4 vecmat [K,N], 6 split-K decode GEMV, 7 row-block decode GEMV, 8
  * 32x32x16 prefill GEMM, 9 fp32 vecmat, 10 32x32x16 prefill GEMM with K split
- * over workgroups, 11 128-row int4 prefill GEMM. */
+ * over workgroups, 11 register-dequant 16x16x32 prefill GEMM. */
 MQ_API int mq_last_path(void);
 
 MQ_API const char* mq_last_error(void);

@@ -51,16 +51,16 @@ int num_cus_current() {
 // Path ids (mq_last_path / force_path); 1 and 5 are retired ids of earlier
 // decode kernels and are not reused.
 // PATH_TILED selects the prefill GEMM family (force_path); the kernel that ran
-// is reported as PATH_GEMM16 (the 128-row int4 GEMM), PATH_GEMMW
+// is reported as PATH_GEMM16 (the 16x16x32 register-dequant GEMM), PATH_GEMMW
 // (register-operand 32x32x16 GEMM), PATH_GEMMW_SPLIT (the same with K split
 // over workgroups) or PATH_TILED (the 16x16x32 fallback).
 enum Path {
   PATH_AUTO = 0, PATH_TILED = 2, PATH_GENERIC = 3, PATH_VECMAT_KN = 4, PATH_DECODE = 6, PATH_ROWS = 7,
   PATH_GEMMW = 8, PATH_VECMAT32 = 9, PATH_GEMMW_SPLIT = 10, PATH_GEMM16 = 11
 };
-// prefill GEMM choice (gemm_impl): 0 automatic (the 128-row int4 GEMM where
+// prefill GEMM choice (gemm_impl): 0 automatic (the register-dequant GEMM where
 // its tiles fill the GPU, else the register-operand 32x32x16 kernel where it
-// takes the shape), 1 always the 16x16x32 tiled kernel, 2 the 128-row int4
+// takes the shape), 1 always the 16x16x32 tiled kernel, 2 the register-dequant
 // GEMM wherever it takes the shape
 std::atomic<int> g_gemm_impl{0};
 // gemm_split: 1 lets the 32x32x16 kernel split K over workgroups where its
@@ -128,13 +128,16 @@ bool prefill_ok(const mq::LinearArgs& a) {
   return mq::gemm16_supported(a) || mq::gemmw_supported(a, num_cus_current()) || mq::tiled_supported(a);
 }
 
-// The 128-row int4 GEMM, automatically: where its tiles cover the CUs at
-// least three quarters of the way and its 128-row blocks are at least three
-// quarters full (config 3, M = 512: 256 tiles on 256 CUs).  Smaller grids go
-// to the 32x32x16 kernel, whose planner picks narrower tiles or splits K.
+// The 16x16x32 GEMM (mq_gemm16.hip), automatically: where its tiles cover
+// the CUs at least three quarters of the way and its row blocks (128 rows;
+// 64 for int8 SwiGLU up to M = 64) are at least three quarters full
+// (config 3, M = 512: 256 tiles on 256 CUs; config 4, M = 64: 237 tiles).
+// Smaller grids go to the 32x32x16 kernel, whose planner picks narrower
+// tiles or splits K.
 bool gemm16_auto(const mq::LinearArgs& a) {
   if (!mq::gemm16_supported(a)) return false;
-  const int64_t mpad = (int64_t)((a.M + 127) / 128) * 128;
+  const int bm = mq::gemm16_rows_per_tile(a);
+  const int64_t mpad = (int64_t)((a.M + bm - 1) / bm) * bm;
   return 4 * (int64_t)mq::gemm16_workgroups(a) >= 3 * (int64_t)num_cus_current() && 4 * (int64_t)a.M >= 3 * mpad;
 }
 

@@ -109,6 +109,7 @@ hipError_t gemmw_launch(const LinearArgs& a, int num_cus, void* ws, hipStream_t 
 // workspace).  trace: optional per-wave timestamps (null in the library).
 bool gemm16_supported(const LinearArgs& a);
 int gemm16_workgroups(const LinearArgs& a);
+int gemm16_rows_per_tile(const LinearArgs& a);
 hipError_t gemm16_launch(const LinearArgs& a, hipStream_t s, uint64_t* trace);
 
 // 16x16x32 MFMA GEMM, K steps of 32 (fallback for shapes the GEMM above does not take).

@@ -27,7 +27,7 @@ GOLD = os.path.join(os.path.dirname(__file__), "golden", "known_answers.npz")
 
 PATHS = {"tiled": 2, "generic": 3, "decode": 6, "rows": 7}
 # force_path "tiled" selects the prefill GEMM family; the kernel that ran is
-# reported as "gemm16" (128-row int4 GEMM), "gemmw" (register-operand GEMM) or
+# reported as "gemm16" (register-dequant 16x16x32 GEMM), "gemmw" (register-operand GEMM) or
 # "tiled" (16x16x32 fallback)
 FAMILY = {"gemmw": "tiled", "gemmw_split": "tiled", "gemm16": "tiled"}
 
@@ -302,6 +302,8 @@ def test_config4_int8_swiglu(mn, gpu, M):
         if path == "rows" and taken != "rows":
             continue  # activations do not fit in LDS at this M
         assert y.shape == (M, F) and taken == path
+        if M == 64:
+            assert mn.last_path() == "gemm16", mn.last_path()
         check_swiglu(y, acc, f"config4 M={M} [{path}, {mn.last_path()}]")
 
 
@@ -963,7 +965,7 @@ def test_one_hot_selects_dequantized_weights(mn, gpu, qt, path, impl, M):
 
 
 # ---------------------------------------------------------------------------
-# the 128-row int4 prefill GEMM (gemm16)
+# the register-dequant 16x16x32 prefill GEMM (gemm16)
 # ---------------------------------------------------------------------------
 
 @pytest.mark.parametrize("M,K,N,g,epi", [
@@ -977,7 +979,7 @@ def test_one_hot_selects_dequantized_weights(mn, gpu, qt, path, impl, M):
     (1, 512, 160, 128, None),
 ])
 def test_gemm16(mn, gpu, M, K, N, g, epi):
-    """The 128-row int4 GEMM forced on ragged, grouped and per-channel
+    """The register-dequant GEMM (int4) forced on ragged, grouped and per-channel
     shapes with every element-wise epilogue: within the bound of the
     oracle's fp32-accumulated result, and bit-identical on a second run
     (the four partial tiles of a workgroup are summed in a fixed order)."""
@@ -1033,18 +1035,59 @@ def test_gemm16_strided_output_and_inplace_residual(mn, gpu):
     assert (rest == 0).all(), "a store reached past the output's columns"
 
 
+@pytest.mark.parametrize("M,K,N,g,swiglu", [
+    (64, 3584, 2 * 1200, 3584, True),   # config 4's layout at a narrower F (15 tiles of 80)
+    (50, 1024, 2 * 328, 128, True),     # ragged M and F, grouped scales
+    (7, 512, 2 * 96, 64, True),
+    (64, 2048, 2 * 160, 64, True),
+    (200, 1024, 1000, 1024, False),     # 128-row int8 tiles, ragged
+    (512, 3072, 640, 128, False),
+])
+def test_gemm16_int8(mn, gpu, M, K, N, g, swiglu):
+    """The register-dequant GEMM on int8 weights: 64-row tiles of 80 gate +
+    80 up columns with the fused SwiGLU (M <= 64), and 128-row tiles without
+    it; within the bound of the oracle's fp32-accumulated result and
+    bit-identical on a second run."""
+    say(f"gemm16 int8 M={M} K={K} N={N} g={g} swiglu={swiglu}")
+    x, q, s8, z8, g8 = O.make_int8_problem(M, K, N, seed=M + K + N, g=g)
+    rng = np.random.default_rng(K)   # scales that vary per group, nonzero zeros
+    s8 = rng.uniform(0.001, 0.01, s8.shape).astype(np.float16)
+    z8 = rng.uniform(-0.01, 0.01, s8.shape).astype(np.float16)
+    acc = O.matmul_f32acc(x, O.dequant_int8(q, s8, z8, K, g8))
+    kw = {"epilogue": "swiglu"} if swiglu else {}
+    mn.set_option("gemm_impl", 2)
+    try:
+        y, _ = run_dm(mn, gpu, x, q, s8, z8, g8, "int8", "tiled", **kw)
+        ran = mn.last_path()
+        y2, _ = run_dm(mn, gpu, x, q, s8, z8, g8, "int8", "tiled", **kw)
+    finally:
+        mn.set_option("gemm_impl", 0)
+    assert ran == "gemm16", ran
+    if swiglu:
+        assert y.shape == (M, N // 2)
+        check_swiglu(y, acc, "gemm16 int8 swiglu")
+    else:
+        check_close(y, acc, "gemm16 int8")
+    np.testing.assert_array_equal(y2.view(np.uint16), y.view(np.uint16))
+
+
 def test_gemm16_unsupported_shapes_fall_back(mn, gpu):
-    """K % 64 != 0 and int8 weights are not taken by the 128-row GEMM even
-    when it is forced: the prefill family's other kernels run them."""
+    """K % 64 != 0, int4 SwiGLU and int8 SwiGLU above 64 rows are not taken
+    by the register-dequant GEMM even when it is forced: the prefill family's
+    other kernels run them."""
     mn.set_option("gemm_impl", 2)
     try:
         x, wp, s, z = O.make_int4_problem(128, 3104, 256, 32, seed=1)
         y, _ = run_dm(mn, gpu, x, wp, s, z, 32, "int4", "tiled")
         assert mn.last_path() in ("gemmw", "gemmw_split", "tiled"), mn.last_path()
         check_close(y, O.matmul_f32acc(x, O.dequant_int4(wp, s, z, 3104, 32)), "gemm16 fallback int4")
-        x, q, s8, z8, g8 = O.make_int8_problem(128, 1024, 256, seed=2)
-        y, _ = run_dm(mn, gpu, x, q, s8, z8, g8, "int8", "tiled")
+        x, wp, s, z = O.make_int4_problem(64, 1024, 512, 64, seed=3)
+        y, _ = run_dm(mn, gpu, x, wp, s, z, 64, "int4", "tiled", epilogue="swiglu")
         assert mn.last_path() in ("gemmw", "gemmw_split", "tiled"), mn.last_path()
-        check_close(y, O.matmul_f32acc(x, O.dequant_int8(q, s8, z8, 1024, g8)), "gemm16 fallback int8")
+        check_swiglu(y, O.matmul_f32acc(x, O.dequant_int4(wp, s, z, 1024, 64)), "gemm16 fallback int4 swiglu")
+        x, q, s8, z8, g8 = O.make_int8_problem(128, 1024, 512, seed=2)
+        y, _ = run_dm(mn, gpu, x, q, s8, z8, g8, "int8", "tiled", epilogue="swiglu")
+        assert mn.last_path() in ("gemmw", "gemmw_split", "tiled"), mn.last_path()
+        check_swiglu(y, O.matmul_f32acc(x, O.dequant_int8(q, s8, z8, 1024, g8)), "gemm16 fallback int8 swiglu")
     finally:
         mn.set_option("gemm_impl", 0)
