@@ -235,7 +235,8 @@ MQ_API int mq_read_probe(const void* p, int64_t bytes, void* sink, void* stream)
 
 /* Kernel-path override and layout knobs for tests and tuning (no reference
  * counterpart).  Keys: "force_path" (0 automatic, 2 the prefill GEMM family,
- * 3 generic, 6 split-K decode GEMV, 7 row-block decode GEMV), "gemv_steps"
+ * 3 generic, 6 split-K decode GEMV, 7 row-block decode GEMV, 12 register-
+ * streamed decode GEMV: int4, 3 <= M <= 16), "gemv_steps"
  * (K steps per wavefront of the split-K GEMV, 1..8, 0 automatic),
  * "gemv_tiles_per_wg" (row tiles per workgroup: 1, 2 or 4, 0 automatic),
  * "gemm_impl" (prefill GEMM kernel: 0 automatic -- the register-dequant
@@ -254,7 +255,8 @@ MQ_API int mq_set_option(const char* key, int64_t value);
  * mq_vecmat_f32 call on this thread launched: 2 16x16x32 tiled GEMM, 3
  * generic, 4 vecmat [K,N], 6 split-K decode GEMV, 7 row-block decode GEMV, 8
  * 32x32x16 prefill GEMM, 9 fp32 vecmat, 10 32x32x16 prefill GEMM with K split
- * over workgroups, 11 register-dequant 16x16x32 prefill GEMM. */
+ * over workgroups, 11 register-dequant 16x16x32 prefill GEMM, 12
+ * register-streamed decode GEMV. */
 MQ_API int mq_last_path(void);
 
 MQ_API const char* mq_last_error(void);

@@ -19,7 +19,7 @@ OUT_DIR = os.path.join(HERE, "metal_native")
 LIB_NAME = "libmetal_native_amd.so"
 BUILD_DIR = os.path.join(HERE, "_build")
 
-SOURCES = ["mq_capi.cpp", "mq_gemv.hip", "mq_rows.hip", "mq_gemmw.hip", "mq_gemm16.hip", "mq_tiled.hip", "mq_misc.hip", "mq_quant.hip", "mq_glue.hip", "mq_vecmat32.hip"]
+SOURCES = ["mq_capi.cpp", "mq_gemv.hip", "mq_rows.hip", "mq_rstream.hip", "mq_gemmw.hip", "mq_gemm16.hip", "mq_tiled.hip", "mq_misc.hip", "mq_quant.hip", "mq_glue.hip", "mq_vecmat32.hip"]
 
 HIP_FLAGS = [
     "-O3", "-std=c++17", "-fPIC", "--offload-arch=gfx950",

@@ -56,7 +56,7 @@ int num_cus_current() {
 // over workgroups) or PATH_TILED (the 16x16x32 fallback).
 enum Path {
   PATH_AUTO = 0, PATH_TILED = 2, PATH_GENERIC = 3, PATH_VECMAT_KN = 4, PATH_DECODE = 6, PATH_ROWS = 7,
-  PATH_GEMMW = 8, PATH_VECMAT32 = 9, PATH_GEMMW_SPLIT = 10, PATH_GEMM16 = 11
+  PATH_GEMMW = 8, PATH_VECMAT32 = 9, PATH_GEMMW_SPLIT = 10, PATH_GEMM16 = 11, PATH_RSTREAM = 12
 };
 // prefill GEMM choice (gemm_impl): 0 automatic (the register-dequant GEMM where
 // its tiles fill the GPU, else the register-operand 32x32x16 kernel where it
@@ -144,6 +144,7 @@ bool gemm16_auto(const mq::LinearArgs& a) {
 int choose_path(const mq::LinearArgs& a, bool noalloc) {
   int forced = g_force_path.load();
   if (forced == PATH_ROWS && rows_ok(a)) return PATH_ROWS;
+  if (forced == PATH_RSTREAM && mq::rstream_plan(a, num_cus_current()).ok) return PATH_RSTREAM;
   if (forced == PATH_DECODE && decode_ok(a)) return PATH_DECODE;
   if (forced == PATH_TILED && prefill_ok(a)) return PATH_TILED;
   if (forced == PATH_GENERIC) return PATH_GENERIC;
@@ -156,6 +157,11 @@ int choose_path(const mq::LinearArgs& a, bool noalloc) {
     const mq::RowsPlan pl = mq::rows_plan(a, num_cus_current());
     if (pl.ok && pl.KP == 1) return PATH_ROWS;
   }
+  // M = 5..8 whose activations do not fit in LDS whole: the register-streamed
+  // GEMV (no K parts, no workspace; config 2 at M = 5 / 8: 15.0 / 16.1 us
+  // against 17.0 / 18.5 us for the row-block kernel's K parts and 17.6 us
+  // for the split-K GEMV at M = 8)
+  if (a.M >= 5 && a.M <= 8 && mq::rstream_plan(a, num_cus_current()).ok) return PATH_RSTREAM;
   // M = 9..16 with long rows: the prefill GEMM with K split over
   // workgroups beats the split-K GEMV (measured at K >= 8192 on 6 shapes at
   // M = 9, 12, 13-16: faster on all but K = 8192, N = 4096 (2-10 % slower
@@ -190,7 +196,10 @@ int run_linear(const mq::LinearArgs& a, hipStream_t s, bool noalloc = false) {
       path = decode_ok(a) ? PATH_DECODE : PATH_GENERIC;
     }
   }
-  if (path == PATH_ROWS) {
+  if (path == PATH_RSTREAM) {
+    const mq::RsPlan pl = mq::rstream_plan(a, num_cus_current());
+    e = pl.ok ? mq::rstream_launch(a, pl, s) : hipErrorInvalidValue;
+  } else if (path == PATH_ROWS) {
   } else if (path == PATH_DECODE) {
     const mq::GemvPlan pl = mq::gemv_plan(a, num_cus_current(), gemv_tuning());
     void* ws = nullptr;
@@ -609,8 +618,8 @@ MQ_API int mq_set_option(const char* key, int64_t value) {
   if (!key) return fail(MQ_INVALID_ARGUMENT, "set_option: null key");
   if (std::strcmp(key, "force_path") == 0) {
     if (value != PATH_AUTO && value != PATH_TILED && value != PATH_GENERIC && value != PATH_DECODE &&
-        value != PATH_ROWS)
-      return fail(MQ_INVALID_ARGUMENT, "set_option: force_path must be 0, 2, 3, 6 or 7");
+        value != PATH_ROWS && value != PATH_RSTREAM)
+      return fail(MQ_INVALID_ARGUMENT, "set_option: force_path must be 0, 2, 3, 6, 7 or 12");
     g_force_path.store((int)value);
     return MQ_SUCCESS;
   }

@@ -97,6 +97,15 @@ struct RowsPlan {
 RowsPlan rows_plan(const LinearArgs& a, int num_cus, bool allow_split = true);
 hipError_t rows_launch(const LinearArgs& a, const RowsPlan& p, void* ws, hipStream_t s);
 
+// Register-streamed row-block decode GEMV (mq_rstream.hip): int4 weights,
+// 3 <= M <= 16, long K, no workspace.
+struct RsPlan {
+  int rpw, twm, R, TW, KS, nwg;
+  bool ok;
+};
+RsPlan rstream_plan(const LinearArgs& a, int num_cus);
+hipError_t rstream_launch(const LinearArgs& a, const RsPlan& p, hipStream_t s);
+
 // Register-operand 32x32x16 MFMA GEMM (prefill default).  Where its tiles
 // leave CUs idle it may split K over several workgroups per tile (only when
 // allow_split), which needs a zeroed workspace of gemmw_ws_bytes (counters

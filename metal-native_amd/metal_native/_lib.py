@@ -32,7 +32,7 @@ EPILOGUE_RESIDUAL = 4
 EPILOGUE_SWIGLU = 5
 
 PATH_NAMES = {0: "none", 2: "tiled", 3: "generic", 4: "vecmat_kn", 6: "decode", 7: "rows", 8: "gemmw", 9: "vecmat_f32", 10: "gemmw_split",
-              11: "gemm16"}
+              11: "gemm16", 12: "rstream"}
 
 _c_void_p = ctypes.c_void_p
 _i64 = ctypes.c_int64

@@ -25,7 +25,7 @@ TOL_ABS = 1e-2
 TOL_REL = 1e-3
 GOLD = os.path.join(os.path.dirname(__file__), "golden", "known_answers.npz")
 
-PATHS = {"tiled": 2, "generic": 3, "decode": 6, "rows": 7}
+PATHS = {"tiled": 2, "generic": 3, "decode": 6, "rows": 7, "rstream": 12}
 # force_path "tiled" selects the prefill GEMM family; the kernel that ran is
 # reported as "gemm16" (register-dequant 16x16x32 GEMM), "gemmw" (register-operand GEMM) or
 # "tiled" (16x16x32 fallback)
@@ -236,7 +236,9 @@ def test_config2_qwen7b_down(mn, gpu, M):
     K, N, g = 18944, 3584, 128
     x, wp, s, z = O.make_int4_problem(M, K, N, g, seed=0)
     ref = O.matmul_f32acc(x, O.dequant_int4(wp, s, z, K, g))
-    for path in ("rows", "decode", "tiled"):
+    for path in ("rows", "decode", "tiled", "rstream"):
+        if path == "rstream" and M < 3:
+            continue  # the register-streamed GEMV takes M >= 3
         y, taken = run_dm(mn, gpu, x, wp, s, z, g, "int4", path)
         if path == "rows" and taken != "rows":
             continue  # activations do not fit in LDS at this M
@@ -245,7 +247,7 @@ def test_config2_qwen7b_down(mn, gpu, M):
 
 
 @pytest.mark.parametrize("M,K,N,want", [(16, 18944, 3584, "gemmw_split"), (9, 18944, 3584, "gemmw_split"),
-                                         (8, 18944, 3584, "decode"), (16, 4096, 4096, "decode"),
+                                         (8, 18944, 3584, "rstream"), (16, 4096, 4096, "decode"),
                                          (32, 18944, 3584, "gemmw_split")])
 def test_mid_band_routing(mn, gpu, M, K, N, want):
     """Between the decode GEMVs and the prefill GEMM: at M = 9..16 with K >=
@@ -962,6 +964,61 @@ def test_one_hot_selects_dequantized_weights(mn, gpu, qt, path, impl, M):
                                    f"weights, e.g. {y[bad][:4]} vs {ref[bad][:4]}")
     finally:
         mn.set_option("gemm_impl", 0)
+
+
+# ---------------------------------------------------------------------------
+# the register-streamed decode GEMV (rstream)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("M,K,N,g,epi", [
+    (8, 18944, 3584, 128, None),       # config 2 at M = 8 (the automatic route for M = 5..8 there)
+    (5, 18944, 3584, 128, "bias"),
+    (3, 4096, 1000, 64, "residual"),   # ragged rows per workgroup
+    (7, 2944, 777, 128, "bias_silu"),  # K not a multiple of the K step, N odd
+    (4, 2048, 512, 2048, None),        # per-channel scales
+    (6, 1024, 40, 128, "bias_relu"),   # fewer rows than CUs
+    (8, 512, 2 * 640, 64, "swiglu"),
+])
+def test_rstream(mn, gpu, M, K, N, g, epi):
+    """The register-streamed GEMV forced on ragged, grouped and per-channel
+    shapes with the element-wise epilogues and SwiGLU: within the bound of
+    the oracle's fp32-accumulated result, and bit-identical on a second run
+    (the waves' partials are summed in wave order)."""
+    say(f"rstream M={M} K={K} N={N} g={g} {epi}")
+    x, wp, s, z = O.make_int4_problem(M, K, N, g, seed=M * 7 + K + N)
+    acc = O.matmul_f32acc(x, O.dequant_int4(wp, s, z, K, g))
+    kw, b, res = {}, None, None
+    if epi in ("bias", "bias_relu", "bias_silu"):
+        b = np.random.default_rng(N).standard_normal(N).astype(np.float16)
+        kw = {"epilogue": epi, "bias": dev(b, gpu)}
+    elif epi == "residual":
+        res = np.random.default_rng(M).standard_normal((M, N)).astype(np.float16)
+        kw = {"epilogue": "residual", "residual": dev(res, gpu)}
+    elif epi == "swiglu":
+        kw = {"epilogue": "swiglu"}
+    y, taken = run_dm(mn, gpu, x, wp, s, z, g, "int4", "rstream", **kw)
+    y2, _ = run_dm(mn, gpu, x, wp, s, z, g, "int4", "rstream", **kw)
+    assert taken == "rstream", taken
+    if epi is None:
+        check_close(y, acc, "rstream")
+    elif epi == "swiglu":
+        check_swiglu(y, acc, "rstream swiglu")
+    else:
+        check_epilogue(y, acc, epi, f"rstream {epi}", bias=b, residual=res)
+    np.testing.assert_array_equal(y2.view(np.uint16), y.view(np.uint16))
+
+
+def test_rstream_declines_what_it_cannot_take(mn, gpu):
+    """int8 weights and M above 16 are not taken by the register-streamed
+    GEMV even when it is forced."""
+    x, q, s8, z8, g8 = O.make_int8_problem(4, 1024, 256, seed=3)
+    y, taken = run_dm(mn, gpu, x, q, s8, z8, g8, "int8", "rstream")
+    assert taken != "rstream", taken
+    check_close(y, O.matmul_f32acc(x, O.dequant_int8(q, s8, z8, 1024, g8)), "rstream fallback int8")
+    x, wp, s, z = O.make_int4_problem(17, 1024, 256, 32, seed=4)
+    y, taken = run_dm(mn, gpu, x, wp, s, z, 32, "int4", "rstream")
+    assert taken != "rstream", taken
+    check_close(y, O.matmul_f32acc(x, O.dequant_int4(wp, s, z, 1024, 32)), "rstream fallback M=17")
 
 
 # ---------------------------------------------------------------------------
