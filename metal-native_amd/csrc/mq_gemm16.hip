@@ -17,11 +17,12 @@
 //    K-tiles, so every weight is loaded and dequantized once per workgroup
 //    and every activation moved once.
 //  * Activations: direct-to-LDS 16-byte loads (buffer_load ... lds), fully
-//    coalesced, in a ring of NS slots per wave (2 of 16 KiB for 128-row
-//    tiles, 4 of 8 KiB for 64-row tiles), XOR-swizzled so that the fragment
-//    reads (one row per lane) are bank-conflict free.  A K-tile's second
-//    k-step fragments are read first, so its slot is refilled (K-tile t+NS)
-//    while its first k-step computes.
+//    coalesced, in a ring of 2 slots per wave (16 KiB for 128-row tiles,
+//    8 KiB for 64-row tiles; 32 KiB per wave in all, the rest used by the
+//    partial exchange), XOR-swizzled so that the fragment reads (one row per
+//    lane) are bank-conflict free.  A K-tile's second k-step fragments are
+//    read first, so its slot is refilled (K-tile t+2) while its first k-step
+//    computes.
 //  * Weights: lane (c, q) of block j loads the 16 k at 64t + 16q of its
 //    column (8 bytes int4, 16 bytes int8): the first half is its B operand
 //    of the tile's first k-step, the second half of the second (k-step s
@@ -117,11 +118,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   constexpr int BNO = 16 * NBU;                 // output columns per tile
   constexpr int BM = 16 * MBK;                  // rows per tile
   constexpr int SLOTU = BM * 8;                 // 16-byte pieces per activation slot (BM rows x 64 k)
-  constexpr int NS = G16_AU / SLOTU;            // activation slots per wave
+  constexpr int NS = G16_AU / SLOTU;            // 16-byte slots of the wave's activation space
+  // activation ring depth: 2 slots (one K-tile of lead beyond the current);
+  // with a 2-deep weight ring too the K-tile loop is unrolled by 2, so a
+  // wave's last K-tiles fill the unroll (int8: 14 K-tiles per wave at config
+  // 4, which a 4-tile unroll would round up to 16)
+  constexpr int NSA = WPF == 2 ? 2 : NS;
+  constexpr int UNR = WPF > NSA ? WPF : NSA;     // K-tiles per loop iteration
   constexpr int NDMA = 2 * MBK;                 // DMA instructions per K-tile (8 rows each)
   constexpr int WB = FMT == FMT_INT4 ? 8 : 16;  // weight bytes per lane per K-tile
   constexpr int NRANGE = SWI ? 2 : 1;           // weight row ranges (gate, up)
-  static_assert(NS == 2 || NS == 4, "the K-tile loop is unrolled by 4");
+  static_assert(NS == 2 || NS == 4, "the activation space is 2 or 4 slots");
+  static_assert(UNR == 2 || UNR == 4, "the K-tile loop is unrolled by 2 or 4");
   static_assert(!SWI || NB % 2 == 0, "SwiGLU pairs gate and up blocks");
   static_assert(MBK * NB - (MBK * NB) / 4 <= 32, "a wave's partials fit in its activation space");
   typedef typename std::conditional<FMT == FMT_INT4, u2v, u4>::type WReg;
@@ -400,31 +408,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     }
   }
 
-  // K-tile t (t - kt0 = R mod 4): activations in slot R % NS, weights in
-  // ring slot R % WPF; the next K-tile's activations are in slot (R+1) % NS.
+  // K-tile t (t - kt0 = R mod UNR): activations in slot R % NSA, weights in
+  // ring slot R % WPF; the next K-tile's activations are in slot (R+1) % NSA.
   auto tile = [&](auto rc, int t) {
     constexpr int R = decltype(rc)::value;
     constexpr int RW = R % WPF, RW1 = (R + 1) % WPF;
-    u4* const cur = slot(std::integral_constant<int, R % NS>{});
-    u4* const nxt = slot(std::integral_constant<int, (R + 1) % NS>{});
+    u4* const cur = slot(std::integral_constant<int, R % NSA>{});
+    u4* const nxt = slot(std::integral_constant<int, (R + 1) % NSA>{});
     if (R == 0 && t == kt0) {   // the first K-tile: the rest of the prologue
       dma_tile(kt0 + 1, slot(std::integral_constant<int, 1>{}));
-      if constexpr (NS > 2) {
-        dma_tile(kt0 + 2, slot(std::integral_constant<int, 2 % NS>{}));
-        dma_tile(kt0 + 3, slot(std::integral_constant<int, 3 % NS>{}));
+      if constexpr (NSA > 2) {
+        dma_tile(kt0 + 2, slot(std::integral_constant<int, 2 % NSA>{}));
+        dma_tile(kt0 + 3, slot(std::integral_constant<int, 3 % NSA>{}));
       }
 #pragma unroll
       for (int d = 2; d < WPF; ++d) load_w(kt0 + d, wring[d]);
     }
     read_sz(t + 1, sz2);
     // k-step 0 of tile t: reads all of k-step 1's fragments first; once
-    // they are in registers the slot is refilled (K-tile t+NS), spread over
+    // they are in registers the slot is refilled (K-tile t+NSA), spread over
     // the rest of the k-step; then the weight slot is refilled
     step(std::true_type{}, afA, bqA, cur, 1, afB, wring[RW], sz, 1, bqB, [&](int j) {
       if (j == 0) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
       for (int i = 0; i < NDMA; ++i)
-        if ((i * NB) / NDMA == j) dma_one(t + NS, cur, i);
+        if ((i * NB) / NDMA == j) dma_one(t + NSA, cur, i);
     });
     load_w(t + WPF, wring[RW]);
     // k-step 1 of tile t; prepares tile t+1's k-step 0 from slot `nxt`
@@ -432,16 +440,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
     for (int j = 0; j < NB; ++j) sz[j] = sz2[j];
   };
-  // four K-tiles per iteration (static ring indices: no register copies of
+  // UNR K-tiles per iteration (static ring indices: no register copies of
   // loads in flight); a K-tile past the wave's range reads zeros and has
   // zero scales
   int t = kt0;
   do {
     tile(std::integral_constant<int, 0>{}, t);
     tile(std::integral_constant<int, 1>{}, t + 1);
-    tile(std::integral_constant<int, 2>{}, t + 2);
-    tile(std::integral_constant<int, 3>{}, t + 3);
-    t += 4;
+    if constexpr (UNR == 4) {
+      tile(std::integral_constant<int, 2 % UNR>{}, t + 2);
+      tile(std::integral_constant<int, 3 % UNR>{}, t + 3);
+    }
+    t += UNR;
   } while (t < kt1);
   const uint64_t T2 = __builtin_amdgcn_s_memrealtime();
 
