@@ -442,7 +442,7 @@ def main():
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(the kernels shard by weight rows; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+              "(the kernels would shard by weight rows, one shard per GPU). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     import torch
