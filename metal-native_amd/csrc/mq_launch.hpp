@@ -88,7 +88,7 @@ hipError_t gemv_scratch(hipStream_t s, void** ptr);
 // KP > 1 splits K into parts (activations too long for LDS); the parts of a
 // row block meet through ws_bytes of the per-stream workspace.
 struct RowsPlan {
-  int rpw, nw, nwg, R, TW, KS, XS, maxT, snp;
+  int rpw, mh, nw, nwg, R, TW, KS, XS, maxT, snp;   // mh: activation-row halves (2: M = 9..16 on 8-row tiles)
   int KP, nblk, KStot;
   uint32_t off_sz, off_scr, off_slot, off_wft;
   size_t lds_bytes, ws_bytes;

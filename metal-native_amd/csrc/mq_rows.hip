@@ -19,6 +19,10 @@
 //    contiguous bytes.  The A operand holds activation row i % RPW at K shift
 //    i / RPW (needs M <= RPW; RPW = 8 and 16 only for the quantized formats); the
 //    result for (activation i, weight row r) is sum_s D[s*RPW + i][s*RPW + r].
+//    M = 9..16 (quantized, no pre-norm) runs on 8-row tiles with the
+//    activation rows in two halves: each dequantized fragment feeds two
+//    MFMAs, rows 0..7 and 8..15 (16-row tiles would read only 64 bytes of each
+//    of 16 rows per load, and cost 13 % more at config 4, M = 16).
 //  * The workgroup's work is TW tiles x KS K-steps ("units", tile-major); wave
 //    w takes the contiguous units [w*U/NW, (w+1)*U/NW) and streams them
 //    through a ring of D register slots refilled as they are consumed.  Every
@@ -80,7 +84,7 @@ struct RowsKArgs {
   float pre_eps;
 };
 
-template <int FMT, int EPI, int RPW, bool PRE, int NW>
+template <int FMT, int EPI, int RPW, bool PRE, int NW, int MH>
 __global__ __launch_bounds__(64 * NW) void rows_kernel(RowsKArgs p) {
   constexpr int S = 16 / RPW;
   constexpr int KPL = FmtTraits<FMT>::KPL;       // k per 16-byte piece
@@ -360,7 +364,10 @@ __global__ __launch_bounds__(64 * NW) void rows_kernel(RowsKArgs p) {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
   // ---- stream ----
+  // MH activation-row halves (MH = 2: M = 9..16 on 8-row tiles, the second
+  // half's fragments RPW rows further down, the same dequantized weights)
   const int xrow = min(r, M - 1) * p.XS;
+  const int xdh = (min(r + RPW, M - 1) - min(r, M - 1)) * p.XS;
   uint32_t mlo = 0x000F000Fu, mhi = 0x00F000F0u;
   asm volatile("" : "+v"(mlo), "+v"(mhi));  // keep the nibble masks in VGPRs
   const uint32_t magic = 0x64006400u;
@@ -394,22 +401,28 @@ __global__ __launch_bounds__(64 * NW) void rows_kernel(RowsKArgs p) {
   // 64 k per unit) the fragment address is recomputed per unit
   constexpr bool XCONST = KSTEP % 128 == 0;
   constexpr int XADV = KSTEP + (KSTEP >> 7) * 8;
-  f4 acc = (f4){0.f, 0.f, 0.f, 0.f};
+  f4 acc[MH];
+#pragma unroll
+  for (int h = 0; h < MH; ++h) acc[h] = (f4){0.f, 0.f, 0.f, 0.f};
 
   auto flush = [&]() {
-    mfma_result_fence(acc);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) scr[(4 * gi + e) * 16 + nl] = acc[e];
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    for (int idx = lane; idx < M * RPW; idx += 64) {   // one pass but for 16-row tiles
-      const int i = idx / RPW, rr = idx - i * RPW;
-      float v = 0.f;
+    for (int h = 0; h < MH; ++h) {
+      mfma_result_fence(acc[h]);
 #pragma unroll
-      for (int s = 0; s < S; ++s) v += scr[(s * RPW + i) * 16 + s * RPW + rr];
-      slots[(w * p.maxT + (ct - ft)) * (M * RPW) + idx] = v;
+      for (int e = 0; e < 4; ++e) scr[(4 * gi + e) * 16 + nl] = acc[h][e];
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      const int mh = min(M - RPW * h, RPW);   // activation rows of this half
+      for (int idx = lane; idx < mh * RPW; idx += 64) {   // one pass but for 16-row tiles
+        const int i = idx / RPW, rr = idx - i * RPW;
+        float v = 0.f;
+#pragma unroll
+        for (int s = 0; s < S; ++s) v += scr[(s * RPW + i) * 16 + s * RPW + rr];
+        slots[(w * p.maxT + (ct - ft)) * (M * RPW) + RPW * RPW * h + idx] = v;
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      acc[h] = (f4){0.f, 0.f, 0.f, 0.f};
     }
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    acc = (f4){0.f, 0.f, 0.f, 0.f};
   };
 
   auto step = [&](const u4 v) {
@@ -436,8 +449,11 @@ __global__ __launch_bounds__(64 * NW) void rows_kernel(RowsKArgs p) {
       } else {
         bq = __builtin_bit_cast(h8, v);
       }
-      const h8 a = *(const h8*)(xa + 8 * j);
-      acc = mfma16x16x32(a, bq, acc);
+#pragma unroll
+      for (int h = 0; h < MH; ++h) {
+        const h8 a = *(const h8*)(xa + h * xdh + 8 * j);
+        acc[h] = mfma16x16x32(a, bq, acc[h]);
+      }
     }
   };
 
@@ -571,9 +587,9 @@ __global__ __launch_bounds__(64 * NW) void rows_kernel(RowsKArgs p) {
   }
 }
 
-template <int FMT, int EPI, int RPW, bool PRE, int NW>
+template <int FMT, int EPI, int RPW, bool PRE, int NW, int MH>
 hipError_t launch5(const RowsKArgs& k, const RowsPlan& pl, hipStream_t s) {
-  auto fn = rows_kernel<FMT, EPI, RPW, PRE, NW>;
+  auto fn = rows_kernel<FMT, EPI, RPW, PRE, NW, MH>;
   hipError_t e = allow_dynamic_lds((const void*)fn, (int)kLds);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(fn, dim3(pl.nwg), dim3(64 * NW), pl.lds_bytes, s, k);
@@ -582,8 +598,15 @@ hipError_t launch5(const RowsKArgs& k, const RowsPlan& pl, hipStream_t s) {
 
 template <int FMT, int EPI, int RPW, bool PRE>
 hipError_t launch4(const RowsKArgs& k, const RowsPlan& pl, hipStream_t s) {
-  if (pl.nw == kNWSmall) return launch5<FMT, EPI, RPW, PRE, kNWSmall>(k, pl, s);
-  if (pl.nw == kNWBig) return launch5<FMT, EPI, RPW, PRE, kNWBig>(k, pl, s);
+  if constexpr (RPW == 8 && !PRE && FMT != FMT_F16) {
+    if (pl.mh == 2) {   // M = 9..16 on 8-row tiles: twelve waves (the activations are large)
+      if (pl.nw == kNWBig) return launch5<FMT, EPI, RPW, PRE, kNWBig, 2>(k, pl, s);
+      return hipErrorInvalidValue;
+    }
+  }
+  if (pl.mh != 1) return hipErrorInvalidValue;
+  if (pl.nw == kNWSmall) return launch5<FMT, EPI, RPW, PRE, kNWSmall, 1>(k, pl, s);
+  if (pl.nw == kNWBig) return launch5<FMT, EPI, RPW, PRE, kNWBig, 1>(k, pl, s);
   return hipErrorInvalidValue;
 }
 
@@ -663,6 +686,16 @@ RowsPlan rows_plan_k(const LinearArgs& a, int num_cus, int KP) {
     const double work = (double)rr * ((a.K + ks - 1) / ks * ks) * pref;
     if (work < best_work) { best_work = work; rpw = cand; }
   }
+  // M = 9..16 (quantized, no pre-norm): 8-row tiles with the activation rows
+  // in two halves (two MFMAs per dequantized fragment) instead of 16-row
+  // tiles, whose per-lane loads cover 64 bytes of each of 16 rows
+  int mh = 1;
+#ifndef MQ_ROWS_NO_MH2
+  if (quant && !a.prenorm && a.M >= 9 && a.M <= 16) {
+    rpw = 8;
+    mh = 2;
+  }
+#endif
   const int S = 16 / rpw;
   const int kstep = 4 * kpl * S;
   const int gran = a.epi == EPI_SWIGLU ? rpw / 2 : rpw;  // output rows per tile
@@ -678,7 +711,7 @@ RowsPlan rows_plan_k(const LinearArgs& a, int num_cus, int KP) {
   if (KP > 1 && (int64_t)KS * (KP - 1) >= KStot) return p;   // every part has steps
   const int U = TW * KS;
   const int64_t wbytes = (int64_t)(a.epi == EPI_SWIGLU ? 2 * R : R) * a.ldw / KP;   // weight bytes per workgroup
-  const int nw = wbytes <= kSmallBytes ? kNWSmall : kNWBig;
+  const int nw = mh == 2 || wbytes > kSmallBytes ? kNWBig : kNWSmall;
   const int per = (U + nw - 1) / nw;
   const int maxT = per / KS + 2;
   if ((int64_t)(a.epi == EPI_SWIGLU ? a.F + R : R) * a.ldw >= lim) return p;
@@ -710,7 +743,7 @@ RowsPlan rows_plan_k(const LinearArgs& a, int num_cus, int KP) {
     if (a.M != 1 || !quant || a.K % 8 || pieces > (int64_t)kXB * 64 * nw || !a.pre_weight || !a.pre_resid) return p;
     if (((uintptr_t)a.pre_weight | (uintptr_t)a.pre_resid | (uintptr_t)a.pre_delta) & 15) return p;
   }
-  p.rpw = rpw; p.nw = nw; p.nwg = nwg; p.R = R; p.TW = TW; p.KS = KS; p.XS = XS; p.maxT = maxT;
+  p.rpw = rpw; p.mh = mh; p.nw = nw; p.nwg = nwg; p.R = R; p.TW = TW; p.KS = KS; p.XS = XS; p.maxT = maxT;
   p.KP = KP; p.nblk = nblk; p.KStot = KStot;
   p.ws_bytes = KP > 1 ? kCntBytesRows + (size_t)KP * nblk * a.M * R * (a.epi == EPI_SWIGLU ? 2 : 1) * 4 : 0;
   if (KP > 1 && (size_t)nblk * 4 > kCntBytesRows) return p;
