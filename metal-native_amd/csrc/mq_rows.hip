@@ -605,7 +605,11 @@ hipError_t launch4(const RowsKArgs& k, const RowsPlan& pl, hipStream_t s) {
     }
   }
   if (pl.mh != 1) return hipErrorInvalidValue;
-  if (pl.nw == kNWSmall) return launch5<FMT, EPI, RPW, PRE, kNWSmall, 1>(k, pl, s);
+  // (int8 with the pre-norm always takes twelve waves: its eight-wave build
+  // spills registers)
+  if constexpr (!(FMT == FMT_INT8 && PRE)) {
+    if (pl.nw == kNWSmall) return launch5<FMT, EPI, RPW, PRE, kNWSmall, 1>(k, pl, s);
+  }
   if (pl.nw == kNWBig) return launch5<FMT, EPI, RPW, PRE, kNWBig, 1>(k, pl, s);
   return hipErrorInvalidValue;
 }
@@ -711,7 +715,7 @@ RowsPlan rows_plan_k(const LinearArgs& a, int num_cus, int KP) {
   if (KP > 1 && (int64_t)KS * (KP - 1) >= KStot) return p;   // every part has steps
   const int U = TW * KS;
   const int64_t wbytes = (int64_t)(a.epi == EPI_SWIGLU ? 2 * R : R) * a.ldw / KP;   // weight bytes per workgroup
-  const int nw = mh == 2 || wbytes > kSmallBytes ? kNWBig : kNWSmall;
+  const int nw = mh == 2 || wbytes > kSmallBytes || (a.prenorm && a.fmt == FMT_INT8) ? kNWBig : kNWSmall;
   const int per = (U + nw - 1) / nw;
   const int maxT = per / KS + 2;
   if ((int64_t)(a.epi == EPI_SWIGLU ? a.F + R : R) * a.ldw >= lim) return p;

@@ -118,10 +118,12 @@ def test_fused_rope_attention_matches_separate_kernels(gpu, H, KVH, D, L, pos):
         assert float(err.max()) <= 1e-3 * (1 + float(want.float().abs().max())), (rep, float(err.max()))
 
 
-@pytest.mark.parametrize("N,K,epi", [(4608, 3584, "bias"), (2 * 18944, 3584, "swiglu"), (3584, 18944, None),
-                                     (1000, 256, None), (640, 512, "swiglu")])
+@pytest.mark.parametrize("N,K,epi,qt", [(4608, 3584, "bias", "int4"), (2 * 18944, 3584, "swiglu", "int4"),
+                                        (3584, 18944, None, "int4"), (1000, 256, None, "int4"),
+                                        (640, 512, "swiglu", "int4"), (4608, 3584, "bias", "int8"),
+                                        (1000, 256, None, "int8"), (640, 512, "swiglu", "int8")])
 @pytest.mark.parametrize("with_delta", [True, False])
-def test_rmsnorm_fused_into_gemv(gpu, N, K, epi, with_delta):
+def test_rmsnorm_fused_into_gemv(gpu, N, K, epi, qt, with_delta):
     """One launch (residual add + RMSNorm in the GEMV's staging) against
     add_rmsnorm followed by dequant_matmul: the residual bit for bit, the
     product within the matmul tolerance."""
@@ -135,16 +137,22 @@ def test_rmsnorm_fused_into_gemv(gpu, N, K, epi, with_delta):
     x = torch.from_numpy(rng.standard_normal((1, K)).astype(np.float16)).to(gpu)
     d = torch.from_numpy(rng.standard_normal((1, K)).astype(np.float16)).to(gpu) if with_delta else None
     w = torch.from_numpy((rng.standard_normal(K) * 0.1 + 1).astype(np.float16)).to(gpu)
-    _, wp, s, z = O.make_int4_problem(1, K, N, 128, seed=K)
+    if qt == "int4":
+        _, wp, s, z = O.make_int4_problem(1, K, N, 128, seed=K)
+        g = 128
+    else:
+        _, wp, s, z, g = O.make_int8_problem(1, K, N, seed=K, g=128)
+        z = rng.uniform(-0.01, 0.01, s.shape).astype(np.float16)
     wp, s, z = (torch.from_numpy(t).to(gpu) for t in (wp, s, z))
     b = torch.from_numpy(rng.standard_normal(N).astype(np.float16)).to(gpu) if epi == "bias" else None
-    assert ops._L.mq_rmsnorm_dequant_matmul_supported(N, K, 128, 0, ops._EPILOGUES[epi]) == 1
+    qc = 0 if qt == "int4" else 1
+    assert ops._L.mq_rmsnorm_dequant_matmul_supported(N, K, g, qc, ops._EPILOGUES[epi]) == 1
     r1 = torch.empty_like(x)
-    y1 = ops.rmsnorm_dequant_matmul(x, d, w, 1e-6, r1, wp, s, z, 128, "int4", epilogue=epi, bias=b)
+    y1 = ops.rmsnorm_dequant_matmul(x, d, w, 1e-6, r1, wp, s, z, g, qt, epilogue=epi, bias=b)
     assert mn.last_path() == "rows"
     r2 = x.clone()
     h = ops.add_rmsnorm(r2, d, w, 1e-6)
-    y2 = mn.dequant_matmul(h, wp, s, z, 128, "int4", epilogue=epi, bias=b)
+    y2 = mn.dequant_matmul(h, wp, s, z, g, qt, epilogue=epi, bias=b)
     assert torch.equal(r1, r2)
     err = (y1.float() - y2.float()).abs()
     assert float(err.max()) <= 2e-2 + 2e-3 * float(y2.float().abs().max()), float(err.max())
