@@ -97,7 +97,9 @@ __global__ __launch_bounds__(kThreads, 2) void tiled_kernel(TiledKArgs p) {
     if (FMT == FMT_INT4) { a0 = perm8_int4(a0); a1 = perm8_int4(a1); }
     *(u4*)as = a0;
     *(u4*)(as + 8) = a1;
-    h2 s2 = (h2){st.s, st.s}, z2 = (h2){st.z, st.z};
+    // (built from the bits: a vector literal of two halves went through scratch memory)
+    const uint32_t su = __builtin_bit_cast(uint16_t, st.s), zu = __builtin_bit_cast(uint16_t, st.z);
+    const h2 s2 = as_h2(su | (su << 16)), z2 = as_h2(zu | (zu << 16));
     if (FMT == FMT_INT4) {
       *(h8*)bs = dq_int4_dword_perm(st.w.x, s2, z2);
       *(h8*)(bs + 8) = dq_int4_dword_perm(st.w.y, s2, z2);
