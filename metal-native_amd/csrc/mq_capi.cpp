@@ -151,7 +151,7 @@ int choose_path(const mq::LinearArgs& a, bool noalloc) {
   // automatic choice: the row-block kernel up to M = 4; for M = 5..16 only
   // where the activations fit in LDS whole (its K parts measured slower than
   // the split-K GEMV at config 2, M = 8: 20.3 vs 18.2 us; whole, it is
-  // faster: config 4 at M = 8, 29.5 vs 40.3 us, at M = 16, 39.6 vs 45.4 us)
+  // faster: config 4 at M = 8, 29.5 vs 40.3 us, at M = 16, 31.8 vs 45.4 us)
   if (a.M <= 4 && rows_ok(a)) return PATH_ROWS;
   if (a.M <= 16) {
     const mq::RowsPlan pl = mq::rows_plan(a, num_cus_current());
