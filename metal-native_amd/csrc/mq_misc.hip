@@ -3,6 +3,8 @@
 #include "mq_device.hpp"
 #include "mq_launch.hpp"
 
+#include <type_traits>
+
 namespace mq {
 namespace {
 
@@ -12,40 +14,53 @@ namespace {
 // B-tile dequant of matmul_dequant_kernel.metal:128-162 (per row, with zero).
 // ---------------------------------------------------------------------------
 
-// Vector path: one thread = one 16-byte piece of a weight row.
+// Vector path: one thread = 8 weights of a row (int4: one 4-byte word,
+// int8: two), written as one 16-byte piece of fp16, so a wavefront's load
+// reads 256 (int4) or 512 (int8) contiguous bytes and its store writes 1 KiB
+// contiguous.  Each thread takes kDqU such pieces a grid apart, every load
+// issued before the first store.  (One thread per 16-byte input piece, i.e.
+// 64 or 32 bytes of output per thread, left each store instruction's lanes
+// 64 or 32 bytes apart: 48.7 vs 37.1 us for the flat int4 dequantize of the
+// config-2 weights.)
+constexpr int kDqU = 4;
+typedef uint32_t u2v __attribute__((ext_vector_type(2)));
 template <int FMT>
-__global__ __launch_bounds__(256) void dequant_vec_kernel(DequantArgs p, int gshift, int64_t pieces,
-                                                          int ppr) {
-  constexpr int KPL = FmtTraits<FMT>::KPL;
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < pieces;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    int n = (int)(i / ppr);
-    int c = (int)(i - (int64_t)n * ppr);
-    int k = c * KPL;
-    int gi = gshift >= 0 ? (k >> gshift) : (p.G == 1 ? 0 : k / p.g);
-    const _Float16* sp = (const _Float16*)p.scales;
-    const _Float16* zp = (const _Float16*)p.zeros;
-    _Float16 s = sp[(int64_t)n * p.G + gi];
-    _Float16 z = zp ? zp[(int64_t)n * p.G + gi] : (_Float16)0.f;
-    h2 s2 = (h2){s, s}, z2 = (h2){z, z};
-    u4 raw = __builtin_nontemporal_load((const u4*)((const unsigned char*)p.W + (int64_t)n * p.ldw + 16 * c));
-    _Float16* out = (_Float16*)p.out + (int64_t)n * p.ldo + k;
-    if (FMT == FMT_INT4) {
-      *(h8*)(out + 0) = dq_int4_dword_nat(raw.x, s2, z2);
-      *(h8*)(out + 8) = dq_int4_dword_nat(raw.y, s2, z2);
-      *(h8*)(out + 16) = dq_int4_dword_nat(raw.z, s2, z2);
-      *(h8*)(out + 24) = dq_int4_dword_nat(raw.w, s2, z2);
-    } else {
-      h2 q[8];
-      dq_int8_dword(raw.x, s2, z2, q[0], q[1]);
-      dq_int8_dword(raw.y, s2, z2, q[2], q[3]);
-      dq_int8_dword(raw.z, s2, z2, q[4], q[5]);
-      dq_int8_dword(raw.w, s2, z2, q[6], q[7]);
-      h8 b0, b1;
-      b0.s01 = q[0]; b0.s23 = q[1]; b0.s45 = q[2]; b0.s67 = q[3];
-      b1.s01 = q[4]; b1.s23 = q[5]; b1.s45 = q[6]; b1.s67 = q[7];
-      *(h8*)(out + 0) = b0;
-      *(h8*)(out + 8) = b1;
+__global__ __launch_bounds__(256) void dequant_vec_kernel(DequantArgs p, int gshift, int64_t pieces, int ppr) {
+  typedef typename std::conditional<FMT == FMT_INT4, uint32_t, u2v>::type In;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  const _Float16* sp = (const _Float16*)p.scales;
+  const _Float16* zp = (const _Float16*)p.zeros;
+  for (int64_t i0 = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i0 < pieces; i0 += kDqU * stride) {
+    In raw[kDqU];
+#pragma unroll
+    for (int u = 0; u < kDqU; ++u) {
+      const int64_t i = i0 + u * stride;
+      if (i < pieces) {
+        const int64_t n = i / ppr;
+        raw[u] = __builtin_nontemporal_load((const In*)((const unsigned char*)p.W + n * p.ldw) + (i - n * ppr));
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kDqU; ++u) {
+      const int64_t i = i0 + u * stride;
+      if (i < pieces) {
+        const int64_t n = i / ppr;
+        const int k = 8 * (int)(i - n * ppr);
+        const int gi = gshift >= 0 ? (k >> gshift) : (p.G == 1 ? 0 : k / p.g);
+        const uint32_t su = __builtin_bit_cast(uint16_t, sp[n * p.G + gi]);
+        const uint32_t zu = zp ? __builtin_bit_cast(uint16_t, zp[n * p.G + gi]) : 0u;
+        const h2 s2 = as_h2(su | (su << 16)), z2 = as_h2(zu | (zu << 16));
+        h8 o;
+        if constexpr (FMT == FMT_INT4) {
+          o = dq_int4_dword_nat(raw[u], s2, z2);
+        } else {
+          h2 q0, q1, q2, q3;
+          dq_int8_dword(raw[u].x, s2, z2, q0, q1);
+          dq_int8_dword(raw[u].y, s2, z2, q2, q3);
+          o.s01 = q0; o.s23 = q1; o.s45 = q2; o.s67 = q3;
+        }
+        *(h8*)((_Float16*)p.out + n * p.ldo + k) = o;
+      }
     }
   }
 }
@@ -245,10 +260,11 @@ hipError_t dequantize_launch(const DequantArgs& a, hipStream_t s) {
   vec = vec && (a.K % kpl == 0) && (a.g % kpl == 0) && !((uintptr_t)a.W & 15) && !(a.ldw & 15) &&
         !((uintptr_t)a.out & 15) && !(a.ldo & 7);
   if (vec) {
-    int ppr = a.K / kpl;
-    int64_t pieces = (int64_t)a.N * ppr;
+    const int ppr = a.K / 8;   // 8-weight pieces per row
+    const int64_t pieces = (int64_t)a.N * ppr;
     hipLaunchKernelGGL((a.fmt == FMT_INT4 ? dequant_vec_kernel<FMT_INT4> : dequant_vec_kernel<FMT_INT8>),
-                       dim3(grid_for(pieces, 256)), dim3(256), 0, s, a, log2_exact(a.g), pieces, ppr);
+                       dim3(grid_for((pieces + kDqU - 1) / kDqU, 256)), dim3(256), 0, s, a, log2_exact(a.g), pieces,
+                       ppr);
   } else {
     hipLaunchKernelGGL(dequant_scalar_kernel, dim3(grid_for((int64_t)a.N * a.K, 256)), dim3(256), 0, s, a);
   }
