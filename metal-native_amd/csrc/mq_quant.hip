@@ -10,13 +10,14 @@
 //   int8, symmetric per group: s = half(max|w| / 127) (1 when 0),
 //     q = clamp(rint(w / s), -127, 127), z = 0.
 // Every step is one IEEE fp32 operation (min/max, correctly rounded division,
-// round-to-nearest-even) or an RNE conversion, so the result is bit-identical
-// to the same steps in numpy.
+// round-to-nearest-even) or an RNE conversion, or (the vector path's w / s) a
+// cheaper sequence proven to give the same integer, so the result is
+// bit-identical to the same steps in numpy.
 //
 // General path: one wavefront per (row, group), the group's elements read
 // coalesced, min/max reduced across the wave, each lane writing whole bytes
 // (int4: a lane owns k pairs, so g must be even).  Vector path (power-of-two
-// g, aligned rows): g/8 lanes per group, 16-byte loads, 4- or 8-byte stores.
+// g, aligned rows): up to 4 16-byte pieces per lane, 4- or 8-byte stores.
 // HBM-bound: 2 bytes read and 0.5 (int4) or 1 (int8) byte written per weight.
 #include "mq_device.hpp"
 #include "mq_launch.hpp"
@@ -91,10 +92,40 @@ __global__ __launch_bounds__(256) void quantize_kernel(QuantizeArgs p) {
   }
 }
 
+// rint(x / s) for the 8 weights of a piece, bit-identical to the IEEE quotient
+// rounded to nearest even, at a fraction of a division's cost.  x and s are
+// fp16 values, so an exact quotient that is not a half-integer lies at least
+// 2^-13 from one, and the correctly rounded fp32 quotient never lands on a
+// half-integer it is not.  t = x * fl(1/s) is within 2^-23 |t| of x / s; every
+// |t| < 256 (all a clamp to [-127, 127] or [0, 15] after adding zp <= 15 can
+// tell apart) is then within 2^-15 of the quotient, so rint(t) is rint(x / s)
+// unless t lies within 2^-14 of a half-integer.  A lane with any such t takes
+// the division for its whole piece (a wave does so about once in 16 for
+// continuous data, and for every exact tie).
+__device__ __forceinline__ void rint_quotients(const h8& v, float sf, float (&q)[8]) {
+  const float r = 1.0f / sf;
+  bool near_half = false;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float t = (float)v[e] * r;
+    q[e] = rintf(t);
+    near_half |= fabsf(t - q[e]) > 0.5f - 0x1p-14f;   // exact: |t - rint(t)| <= 0.5
+  }
+  if (near_half) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) q[e] = rintf((float)v[e] / sf);
+  }
+}
+
 // Vector path (g a power of two in 8..512, K and the row stride multiples of
-// 8, 16-byte aligned rows): L = g/8 lanes per group, each lane one 16-byte
-// piece of 8 weights; a wave covers 64/L groups.  Same arithmetic as above.
-template <int FMT>
+// 8, 16-byte aligned rows): each lane takes P 16-byte pieces of 8 weights of
+// one group, L = g / (8 P) lanes per group, piece i of lane l at weight
+// (i L + l) 8 of the group, so each load and store instruction of a wave
+// covers a contiguous run.  The per-group work (index, range reduction, scale
+// and zero) is shared by 8 P weights.  The group's range is taken in fp16
+// (min, max and |.| of fp16 values are exact, so equal to the fp32 ones) and
+// reduced across the L lanes as one packed (min, -max) pair.
+template <int FMT, int P>
 __global__ __launch_bounds__(256) void quantize_vec_kernel(QuantizeArgs p, int lshift) {
   const int lane = threadIdx.x & 63;
   const int L = 1 << lshift;
@@ -103,27 +134,40 @@ __global__ __launch_bounds__(256) void quantize_vec_kernel(QuantizeArgs p, int l
   const bool live = item < (int64_t)p.N * p.G;
   const int64_t it = live ? item : 0;
   const int n = (int)(it / p.G), j = (int)(it - (int64_t)n * p.G);
-  const int k = j * p.g + (lane & (L - 1)) * 8;
-  const bool have = live && k < p.K;
-  h8 v = {};
-  if (have) v = *(const h8*)((const _Float16*)p.W + (int64_t)n * p.ldw + k);
-  float lo = INFINITY, hi = -INFINITY;
-  if (have) {
+  const int k0 = j * p.g + (lane & (L - 1)) * 8;
+  const _Float16* wr = (const _Float16*)p.W + (int64_t)n * p.ldw;
+  h8 v[P];
+  bool have[P];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float f = (float)v[e];
-      if (FMT == FMT_INT4) {
-        lo = fminf(lo, f);
-        hi = fmaxf(hi, f);
-      } else {
-        hi = fmaxf(hi, fabsf(f));
-      }
+  for (int i = 0; i < P; ++i) {
+    have[i] = live && k0 + i * 8 * L < p.K;
+    v[i] = h8{};
+    if (have[i]) v[i] = *(const h8*)(wr + k0 + i * 8 * L);
+  }
+  // range pair (min, -max) for int4, (-max|w|, -max|w|) for int8; +inf when empty
+  h2 m = as_h2(0x7C007C00u);
+#pragma unroll
+  for (int i = 0; i < P; ++i) {
+    if (!have[i]) continue;
+    if (FMT == FMT_INT4) {
+      const h2 a = __builtin_elementwise_min(v[i].s01, v[i].s23), b = __builtin_elementwise_min(v[i].s45, v[i].s67);
+      const h2 c = __builtin_elementwise_max(v[i].s01, v[i].s23), d = __builtin_elementwise_max(v[i].s45, v[i].s67);
+      const h2 lo2 = __builtin_elementwise_min(a, b), hi2 = __builtin_elementwise_max(c, d);
+      m = __builtin_elementwise_min(
+          m, (h2){__builtin_elementwise_min(lo2.x, lo2.y), -__builtin_elementwise_max(hi2.x, hi2.y)});
+    } else {
+      const uint32_t* u = (const uint32_t*)&v[i];
+      const h2 a = __builtin_elementwise_max(as_h2(u[0] & 0x7FFF7FFFu), as_h2(u[1] & 0x7FFF7FFFu));
+      const h2 b = __builtin_elementwise_max(as_h2(u[2] & 0x7FFF7FFFu), as_h2(u[3] & 0x7FFF7FFFu));
+      const h2 c = __builtin_elementwise_max(a, b);
+      const _Float16 h = -__builtin_elementwise_max(c.x, c.y);
+      m = __builtin_elementwise_min(m, (h2){h, h});
     }
   }
-  for (int o = 1; o < L; o <<= 1) {
-    hi = fmaxf(hi, __shfl_xor(hi, o));
-    if (FMT == FMT_INT4) lo = fminf(lo, __shfl_xor(lo, o));
-  }
+  uint32_t pr = __builtin_bit_cast(uint32_t, m);
+  for (int o = 1; o < L; o <<= 1)
+    pr = __builtin_bit_cast(uint32_t, __builtin_elementwise_min(as_h2(pr), as_h2((uint32_t)__shfl_xor((int)pr, o))));
+  const float lo = (float)as_h2(pr).x, hi = -(float)as_h2(pr).y;
   float sf, zp = 0.f;
   _Float16 s16, z16 = (_Float16)0.f;
   if (FMT == FMT_INT4) {
@@ -141,25 +185,42 @@ __global__ __launch_bounds__(256) void quantize_vec_kernel(QuantizeArgs p, int l
     ((_Float16*)p.scales)[it] = s16;   // [N, G] contiguous: index n*G + j
     ((_Float16*)p.zeros)[it] = z16;
   }
-  if (!have) return;
-  if (FMT == FMT_INT4) {
-    uint32_t word = 0;
+  unsigned char* orow = (unsigned char*)p.out + (int64_t)n * p.ldo;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float q = fminf(fmaxf(rintf((float)v[e] / sf) + zp, 0.f), 15.f);
-      word |= (uint32_t)(int)q << (4 * e);
-    }
-    *(uint32_t*)((unsigned char*)p.out + (int64_t)n * p.ldo + (k >> 1)) = word;
-  } else {
-    uint32_t w0 = 0, w1 = 0;
+  for (int i = 0; i < P; ++i) {
+    if (!have[i]) continue;
+    float q[8];
+    rint_quotients(v[i], sf, q);
+    const int k = k0 + i * 8 * L;
+    if (FMT == FMT_INT4) {
+      uint32_t word = 0;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int q = (int)fminf(fmaxf(rintf((float)v[e] / sf), -127.f), 127.f);
-      if (e < 4) w0 |= (uint32_t)(q & 0xFF) << (8 * e);
-      else w1 |= (uint32_t)(q & 0xFF) << (8 * (e - 4));
+      for (int e = 0; e < 8; ++e) word |= (uint32_t)(int)fminf(fmaxf(q[e] + zp, 0.f), 15.f) << (4 * e);
+      *(uint32_t*)(orow + (k >> 1)) = word;
+    } else {
+      uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int qi = (int)fminf(fmaxf(q[e], -127.f), 127.f);
+        if (e < 4) w0 |= (uint32_t)(qi & 0xFF) << (8 * e);
+        else w1 |= (uint32_t)(qi & 0xFF) << (8 * (e - 4));
+      }
+      *(uint2*)(orow + k) = make_uint2(w0, w1);
     }
-    *(uint2*)((unsigned char*)p.out + (int64_t)n * p.ldo + k) = make_uint2(w0, w1);
   }
+}
+
+template <int FMT>
+void quantize_vec_launch(const QuantizeArgs& a, int b, hipStream_t s) {
+  // b = log2(g / 8); P = min(4, g / 8) pieces per lane (8 measured slower: fewer waves)
+  const int64_t items = (int64_t)a.N * a.G;
+  auto go = [&](auto kern, int lshift) {
+    const int64_t waves = (items + (64 >> lshift) - 1) / (64 >> lshift);
+    hipLaunchKernelGGL(kern, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, a, lshift);
+  };
+  if (b >= 2) go(quantize_vec_kernel<FMT, 4>, b - 2);
+  else if (b == 1) go(quantize_vec_kernel<FMT, 2>, 0);
+  else go(quantize_vec_kernel<FMT, 1>, 0);
 }
 
 }  // namespace
@@ -173,12 +234,8 @@ hipError_t quantize_launch(const QuantizeArgs& a, hipStream_t s) {
                    (a.fmt == FMT_INT4 ? (a.ldo % 4 == 0 && ((uintptr_t)a.out & 3) == 0)
                                       : (a.ldo % 8 == 0 && ((uintptr_t)a.out & 7) == 0));
   if (vec) {
-    const int64_t waves = (items + (64 >> lshift) - 1) / (64 >> lshift);
-    const dim3 grid((unsigned)((waves + 3) / 4));
-    if (a.fmt == FMT_INT4)
-      hipLaunchKernelGGL(quantize_vec_kernel<FMT_INT4>, grid, dim3(256), 0, s, a, lshift);
-    else
-      hipLaunchKernelGGL(quantize_vec_kernel<FMT_INT8>, grid, dim3(256), 0, s, a, lshift);
+    if (a.fmt == FMT_INT4) quantize_vec_launch<FMT_INT4>(a, lshift, s);
+    else quantize_vec_launch<FMT_INT8>(a, lshift, s);
     return hipGetLastError();
   }
   const dim3 grid((unsigned)((items + 3) / 4));

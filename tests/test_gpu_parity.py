@@ -631,7 +631,8 @@ def test_decode_variants(mn, gpu, opts, M, K, N, g, qt, epi):
 
 @pytest.mark.parametrize("qt", ["int4", "int8"])
 @pytest.mark.parametrize("N,K,g", [(12, 256, 64), (7, 200, 32), (33, 1000, 128), (64, 896, 64), (5, 130, 128),
-                                   (3584, 18944, 128), (16, 3584, 3584)])
+                                   (3584, 18944, 128), (16, 3584, 3584), (6, 520, 16), (4, 264, 8),
+                                   (9, 1000, 512), (11, 2048, 256)])
 def test_quantize_bit_exact(mn, gpu, qt, N, K, g):
     say(f"quantize {qt} N={N} K={K} g={g}")
     rng = np.random.default_rng(N + K + g)
@@ -647,6 +648,27 @@ def test_quantize_bit_exact(mn, gpu, qt, N, K, g):
     # and the kernels consume what it produced: dequantize matches the oracle's dequant of it
     W = mn.dequantize(bp, s, z, g, qt, K=K)
     np.testing.assert_array_equal(host(W).view(np.uint16), O.dequantize(obp, os_, oz, K, g, qt).view(np.uint16))
+
+
+@pytest.mark.parametrize("qt", ["int4", "int8"])
+def test_quantize_exact_ties(mn, gpu, qt):
+    """Weights on a grid of quarter (int4) or half (int8) steps of the scale:
+    many quotients are exact half-integers, which must round to even as the IEEE quotient does."""
+    say(f"quantize ties {qt}")
+    rng = np.random.default_rng(5)
+    N, K, g = 64, 1024, 128
+    if qt == "int4":
+        w = (rng.integers(-30, 31, size=(N, K)) / 32).astype(np.float16)
+        w[:, ::g] = -30 / 32   # every group spans [-30/32, 30/32]: s = 1/8, w / s = k / 4
+        w[:, 1::g] = 30 / 32
+    else:
+        w = (rng.integers(-254, 255, size=(N, K)) / 256).astype(np.float16)
+        w[:, ::g] = 254 / 256   # max |w| = 254/256: s = 1/128, w / s = k / 2
+    bp, s, z = mn.quantize(dev(w, gpu), g, qt)
+    obp, os_, oz = O.quantize(w, g, qt)
+    np.testing.assert_array_equal(host(bp).view(np.uint8), obp.view(np.uint8))
+    np.testing.assert_array_equal(host(s).view(np.uint16), os_.view(np.uint16))
+    np.testing.assert_array_equal(host(z).view(np.uint16), oz.view(np.uint16))
 
 
 def test_quantize_strided_input(mn, gpu):
