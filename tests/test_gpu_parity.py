@@ -632,7 +632,7 @@ def test_decode_variants(mn, gpu, opts, M, K, N, g, qt, epi):
 @pytest.mark.parametrize("qt", ["int4", "int8"])
 @pytest.mark.parametrize("N,K,g", [(12, 256, 64), (7, 200, 32), (33, 1000, 128), (64, 896, 64), (5, 130, 128),
                                    (3584, 18944, 128), (16, 3584, 3584), (6, 520, 16), (4, 264, 8),
-                                   (9, 1000, 512), (11, 2048, 256)])
+                                   (9, 1000, 512), (11, 2048, 256), (10, 384, 96), (3, 300, 50)])
 def test_quantize_bit_exact(mn, gpu, qt, N, K, g):
     say(f"quantize {qt} N={N} K={K} g={g}")
     rng = np.random.default_rng(N + K + g)
