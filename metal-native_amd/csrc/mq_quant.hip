@@ -92,29 +92,33 @@ __global__ __launch_bounds__(256) void quantize_kernel(QuantizeArgs p) {
   }
 }
 
-// rint(x / s) for the 8 weights of a piece, bit-identical to the IEEE quotient
-// rounded to nearest even, at a fraction of a division's cost.  x and s are
-// fp16 values, so an exact quotient that is not a half-integer lies at least
-// 2^-13 from one, and the correctly rounded fp32 quotient never lands on a
-// half-integer it is not.  t = x * fl(1/s) is within 2^-23 |t| of x / s; every
-// |t| < 256 (all a clamp to [-127, 127] or [0, 15] after adding zp <= 15 can
-// tell apart) is then within 2^-15 of the quotient, so rint(t) is rint(x / s)
-// unless t lies within 2^-14 of a half-integer.  A lane with any such t takes
-// the division for its whole piece (a wave does so about once in 16 for
-// continuous data, and for every exact tie).
-__device__ __forceinline__ void rint_quotients(const h8& v, float sf, float (&q)[8]) {
+// clamp(rint(x / s) + off, lo, hi) for the 8 weights of a piece, with rint of
+// the IEEE quotient rounded to nearest even, at a fraction of a division's
+// cost.  x and s are fp16 values, so an exact quotient that is not a
+// half-integer lies at least 2^-13 from one, and the correctly rounded fp32
+// quotient never lands on a half-integer it is not.  u = fma(x, fl(1/s), off)
+// is within 2^-24 (|x / s| + |u|) of x / s + off: within 2^-15 for every u
+// that a clamp to [0, 15] or [1, 255] can tell apart (|u|, |x / s| <= 256;
+// beyond, u and x / s + off clamp to the same end), so rint(u)
+// is rint(x / s) + off unless u lies within 2^-14 of a half-integer.  A lane
+// with any such u takes the division for its whole piece (a wave does so about
+// once in 16 for continuous data, and for every exact tie).  off is an
+// integer: int4's zero point, or 128 to make int8's q a byte.
+__device__ __forceinline__ void rint_quotients(const h8& v, float sf, float off, float lo, float hi, float (&q)[8]) {
   const float r = 1.0f / sf;
   bool near_half = false;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const float t = (float)v[e] * r;
-    q[e] = rintf(t);
-    near_half |= fabsf(t - q[e]) > 0.5f - 0x1p-14f;   // exact: |t - rint(t)| <= 0.5
+    const float u = __builtin_fmaf((float)v[e], r, off);
+    q[e] = rintf(u);
+    near_half |= fabsf(u - q[e]) > 0.5f - 0x1p-14f;   // exact: |u - rint(u)| <= 0.5
   }
   if (near_half) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) q[e] = rintf((float)v[e] / sf);
+    for (int e = 0; e < 8; ++e) q[e] = rintf((float)v[e] / sf) + off;
   }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) q[e] = fminf(fmaxf(q[e], lo), hi);
 }
 
 // Vector path (g a power of two in 8..512, K and the row stride multiples of
@@ -190,23 +194,22 @@ __global__ __launch_bounds__(256) void quantize_vec_kernel(QuantizeArgs p, int l
   for (int i = 0; i < P; ++i) {
     if (!have[i]) continue;
     float q[8];
-    rint_quotients(v[i], sf, q);
     const int k = k0 + i * 8 * L;
+    // whole numbers in [0, 255] go to bytes with v_cvt_pk_u8_f32 (exact)
+#define PK(x, b, acc) __builtin_amdgcn_cvt_pk_u8_f32(x, b, acc)
     if (FMT == FMT_INT4) {
-      uint32_t word = 0;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) word |= (uint32_t)(int)fminf(fmaxf(q[e] + zp, 0.f), 15.f) << (4 * e);
-      *(uint32_t*)(orow + (k >> 1)) = word;
+      rint_quotients(v[i], sf, zp, 0.f, 15.f, q);
+      // even k in bytes of one word, odd k in another: nibble pairs by one shift-or
+      const uint32_t ev = PK(q[6], 3, PK(q[4], 2, PK(q[2], 1, PK(q[0], 0, 0u))));
+      const uint32_t od = PK(q[7], 3, PK(q[5], 2, PK(q[3], 1, PK(q[1], 0, 0u))));
+      *(uint32_t*)(orow + (k >> 1)) = ev | (od << 4);
     } else {
-      uint32_t w0 = 0, w1 = 0;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int qi = (int)fminf(fmaxf(q[e], -127.f), 127.f);
-        if (e < 4) w0 |= (uint32_t)(qi & 0xFF) << (8 * e);
-        else w1 |= (uint32_t)(qi & 0xFF) << (8 * (e - 4));
-      }
+      rint_quotients(v[i], sf, 128.f, 1.f, 255.f, q);   // q + 128, then back to two's complement
+      const uint32_t w0 = PK(q[3], 3, PK(q[2], 2, PK(q[1], 1, PK(q[0], 0, 0u)))) ^ 0x80808080u;
+      const uint32_t w1 = PK(q[7], 3, PK(q[6], 2, PK(q[5], 1, PK(q[4], 0, 0u)))) ^ 0x80808080u;
       *(uint2*)(orow + k) = make_uint2(w0, w1);
     }
+#undef PK
   }
 }
 
