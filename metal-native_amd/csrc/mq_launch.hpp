@@ -141,6 +141,24 @@ hipError_t dequantize_launch(const DequantArgs& a, hipStream_t s);
 // Group quantizer (the inverse of the dequant formula): W fp16 [N, K] (row
 // stride ldw elements) -> out int4 [N, K/2] / int8 [N, K] (row stride ldo
 // bytes), scales and zeros fp16 [N, G] contiguous.
+// Division of 32-bit indices below 2^31 by a fixed d >= 1 as a multiply and a
+// shift: q = (i + umulhi(i, mp)) >> l with l = ceil(log2 d) and mp =
+// ceil(2^(32+l) / d) - 2^32.  Exact for every i < 2^31: the multiplier's
+// excess over 2^(32+l) / d adds less than i / 2^(32+l) < 1 / (2 d) to i / d.
+struct Div32 {
+  uint32_t mp;
+  int l;
+  static Div32 make(uint32_t d) {
+    int l = 0;
+    while ((1ull << l) < d) ++l;
+    const unsigned __int128 m = ((((unsigned __int128)1) << (32 + l)) + d - 1) / d;
+    return {(uint32_t)(m - ((unsigned __int128)1 << 32)), l};
+  }
+  __host__ __device__ __forceinline__ uint32_t div(uint32_t i) const {
+    return (i + (uint32_t)(((uint64_t)i * mp) >> 32)) >> l;
+  }
+};
+
 struct QuantizeArgs {
   const void* W; int64_t ldw;
   void* out; int64_t ldo;

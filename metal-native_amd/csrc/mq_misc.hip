@@ -22,30 +22,39 @@ namespace {
 // 64 or 32 bytes of output per thread, left each store instruction's lanes
 // 64 or 32 bytes apart: 48.7 vs 37.1 us for the flat int4 dequantize of the
 // config-2 weights.)
+// Piece i is row i / ppr: a multiply and a shift (Div32) when every index
+// is below 2^31 (I32), else a 64-bit division.
 constexpr int kDqU = 4;
 typedef uint32_t u2v __attribute__((ext_vector_type(2)));
-template <int FMT>
-__global__ __launch_bounds__(256) void dequant_vec_kernel(DequantArgs p, int gshift, int64_t pieces, int ppr) {
+template <int FMT, bool I32>
+__global__ __launch_bounds__(256) void dequant_vec_kernel(DequantArgs p, int gshift, int64_t pieces, int ppr,
+                                                          Div32 dv) {
   typedef typename std::conditional<FMT == FMT_INT4, uint32_t, u2v>::type In;
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  typedef typename std::conditional<I32, uint32_t, int64_t>::type Idx;
+  const Idx stride = (Idx)gridDim.x * blockDim.x;
   const _Float16* sp = (const _Float16*)p.scales;
   const _Float16* zp = (const _Float16*)p.zeros;
-  for (int64_t i0 = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i0 < pieces; i0 += kDqU * stride) {
+  auto row_of = [&](Idx i) -> Idx {
+    if constexpr (I32) return dv.div(i);
+    else return i / ppr;
+  };
+  for (Idx i0 = blockIdx.x * (Idx)blockDim.x + threadIdx.x; i0 < (Idx)pieces; i0 += kDqU * stride) {
     In raw[kDqU];
 #pragma unroll
     for (int u = 0; u < kDqU; ++u) {
-      const int64_t i = i0 + u * stride;
-      if (i < pieces) {
-        const int64_t n = i / ppr;
-        raw[u] = __builtin_nontemporal_load((const In*)((const unsigned char*)p.W + n * p.ldw) + (i - n * ppr));
+      const Idx i = i0 + u * stride;
+      if (i < (Idx)pieces) {
+        const Idx n = row_of(i);
+        raw[u] = __builtin_nontemporal_load((const In*)((const unsigned char*)p.W + (int64_t)n * p.ldw) +
+                                            (i - n * (Idx)ppr));
       }
     }
 #pragma unroll
     for (int u = 0; u < kDqU; ++u) {
-      const int64_t i = i0 + u * stride;
-      if (i < pieces) {
-        const int64_t n = i / ppr;
-        const int k = 8 * (int)(i - n * ppr);
+      const Idx i = i0 + u * stride;
+      if (i < (Idx)pieces) {
+        const int64_t n = (int64_t)row_of(i);
+        const int k = 8 * (int)(i - (Idx)n * (Idx)ppr);
         const int gi = gshift >= 0 ? (k >> gshift) : (p.G == 1 ? 0 : k / p.g);
         const uint32_t su = __builtin_bit_cast(uint16_t, sp[n * p.G + gi]);
         const uint32_t zu = zp ? __builtin_bit_cast(uint16_t, zp[n * p.G + gi]) : 0u;
@@ -262,9 +271,17 @@ hipError_t dequantize_launch(const DequantArgs& a, hipStream_t s) {
   if (vec) {
     const int ppr = a.K / 8;   // 8-weight pieces per row
     const int64_t pieces = (int64_t)a.N * ppr;
-    hipLaunchKernelGGL((a.fmt == FMT_INT4 ? dequant_vec_kernel<FMT_INT4> : dequant_vec_kernel<FMT_INT8>),
-                       dim3(grid_for((pieces + kDqU - 1) / kDqU, 256)), dim3(256), 0, s, a, log2_exact(a.g), pieces,
-                       ppr);
+    const dim3 grid(grid_for((pieces + kDqU - 1) / kDqU, 256));
+    // every index the grid-stride loop forms is below pieces + kDqU * (threads
+    // in the grid): the 32-bit path needs that below 2^31
+    const int64_t threads = (int64_t)grid.x * 256;
+    if (pieces + (int64_t)kDqU * threads < ((int64_t)1 << 31)) {
+      hipLaunchKernelGGL((a.fmt == FMT_INT4 ? dequant_vec_kernel<FMT_INT4, true> : dequant_vec_kernel<FMT_INT8, true>),
+                         grid, dim3(256), 0, s, a, log2_exact(a.g), pieces, ppr, Div32::make((uint32_t)ppr));
+    } else {
+      hipLaunchKernelGGL((a.fmt == FMT_INT4 ? dequant_vec_kernel<FMT_INT4, false> : dequant_vec_kernel<FMT_INT8, false>),
+                         grid, dim3(256), 0, s, a, log2_exact(a.g), pieces, ppr, Div32{0u, 0});
+    }
   } else {
     hipLaunchKernelGGL(dequant_scalar_kernel, dim3(grid_for((int64_t)a.N * a.K, 256)), dim3(256), 0, s, a);
   }

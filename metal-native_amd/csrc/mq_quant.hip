@@ -129,15 +129,16 @@ __device__ __forceinline__ void rint_quotients(const h8& v, float sf, float off,
 // and zero) is shared by 8 P weights.  The group's range is taken in fp16
 // (min, max and |.| of fp16 values are exact, so equal to the fp32 ones) and
 // reduced across the L lanes as one packed (min, -max) pair.
-template <int FMT, int P>
-__global__ __launch_bounds__(256) void quantize_vec_kernel(QuantizeArgs p, int lshift) {
+template <int FMT, int P, bool I32>
+__global__ __launch_bounds__(256) void quantize_vec_kernel(QuantizeArgs p, int lshift, Div32 dg) {
   const int lane = threadIdx.x & 63;
   const int L = 1 << lshift;
   const int64_t wave = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int64_t item = (wave << (6 - lshift)) + (lane >> lshift);   // (row, group)
   const bool live = item < (int64_t)p.N * p.G;
   const int64_t it = live ? item : 0;
-  const int n = (int)(it / p.G), j = (int)(it - (int64_t)n * p.G);
+  // n = it / G: a multiply and a shift when every item index is below 2^31
+  const int n = I32 ? (int)dg.div((uint32_t)it) : (int)(it / p.G), j = (int)(it - (int64_t)n * p.G);
   const int k0 = j * p.g + (lane & (L - 1)) * 8;
   const _Float16* wr = (const _Float16*)p.W + (int64_t)n * p.ldw;
   h8 v[P];
@@ -217,13 +218,16 @@ template <int FMT>
 void quantize_vec_launch(const QuantizeArgs& a, int b, hipStream_t s) {
   // b = log2(g / 8); P = min(4, g / 8) pieces per lane (8 measured slower: fewer waves)
   const int64_t items = (int64_t)a.N * a.G;
-  auto go = [&](auto kern, int lshift) {
+  // the item index of a lane is below the grid's waves * 64 <= items + 256
+  const bool i32 = items + 256 < ((int64_t)1 << 31);
+  const Div32 dg = i32 ? Div32::make((uint32_t)a.G) : Div32{0u, 0};
+  auto go = [&](auto k32, auto k64, int lshift) {
     const int64_t waves = (items + (64 >> lshift) - 1) / (64 >> lshift);
-    hipLaunchKernelGGL(kern, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, a, lshift);
+    hipLaunchKernelGGL(i32 ? k32 : k64, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, a, lshift, dg);
   };
-  if (b >= 2) go(quantize_vec_kernel<FMT, 4>, b - 2);
-  else if (b == 1) go(quantize_vec_kernel<FMT, 2>, 0);
-  else go(quantize_vec_kernel<FMT, 1>, 0);
+  if (b >= 2) go(quantize_vec_kernel<FMT, 4, true>, quantize_vec_kernel<FMT, 4, false>, b - 2);
+  else if (b == 1) go(quantize_vec_kernel<FMT, 2, true>, quantize_vec_kernel<FMT, 2, false>, 0);
+  else go(quantize_vec_kernel<FMT, 1, true>, quantize_vec_kernel<FMT, 1, false>, 0);
 }
 
 }  // namespace
