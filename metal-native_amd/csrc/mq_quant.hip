@@ -106,14 +106,14 @@ __global__ __launch_bounds__(256) void quantize_kernel(QuantizeArgs p) {
 // integer: int4's zero point, or 128 to make int8's q a byte.
 __device__ __forceinline__ void rint_quotients(const h8& v, float sf, float off, float lo, float hi, float (&q)[8]) {
   const float r = 1.0f / sf;
-  bool near_half = false;
+  float dmax = 0.f;   // largest |u - rint(u)| (exact differences, <= 0.5)
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const float u = __builtin_fmaf((float)v[e], r, off);
     q[e] = rintf(u);
-    near_half |= fabsf(u - q[e]) > 0.5f - 0x1p-14f;   // exact: |u - rint(u)| <= 0.5
+    dmax = fmaxf(dmax, fabsf(u - q[e]));
   }
-  if (near_half) {
+  if (dmax > 0.5f - 0x1p-14f) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) q[e] = rintf((float)v[e] / sf) + off;
   }
