@@ -74,6 +74,8 @@ struct G16Args {
   int M, N, K, G, gshift;
   int F;              // output columns: N/2 with SwiGLU, else N
   int nbm, KT, xcd;
+  int SG;             // scale|zero table row stride: G + 1 rounded up to odd (column G is zero)
+  Div32 gdiv;         // division by G
   int vec_store;      // C rows 16-byte aligned: staged 16-byte stores
   uint32_t a_bytes, w_bytes, s_bytes;
   uint64_t* trace;    // optional per-wave timestamps (tests of the schedule only)
@@ -133,7 +135,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   static_assert(!SWI || NB % 2 == 0, "SwiGLU pairs gate and up blocks");
   static_assert(MBK * NB - (MBK * NB) / 4 <= 32, "a wave's partials fit in its activation space");
   typedef typename std::conditional<FMT == FMT_INT4, u2v, u4>::type WReg;
-  __shared__ uint32_t lds_sz[G16_SZT];    // scale | zero << 16 of the tile's weight rows x all groups
+  // scale | zero << 16 of the tile's weight rows x all groups, rows SG apart
+  // (odd: the 16 rows one read touches fall in different banks), column G
+  // zero (read by K-tiles past the wave's range)
+  __shared__ uint32_t lds_sz[G16_SZT];
   const uint64_t T0 = __builtin_amdgcn_s_memrealtime();
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -231,12 +236,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   dma_tile(kt0, slot(std::integral_constant<int, 0>{}));
   load_w(kt0, wring[0]);
   load_w(kt0 + 1, wring[1]);
-  // scale | zero table writes (s | z << 16 per entry; range rg at entry
-  // rg * BNO * G)
+  // scale | zero table writes (s | z << 16 per entry; range rg from row
+  // rg * BNO), then the zero column
+  const int SG = p.SG;
 #pragma unroll
   for (int rg = 0; rg < NRANGE; ++rg) {
     const int e0 = (rg ? p.F + n0 : n0) * p.G;
-    const int d0 = rg * BNO * p.G;
+    const int d0 = rg * BNO * SG;
     const int pb = e0 >> 3, pe = (e0 + cnt + 7) >> 3;
 #pragma unroll
     for (int r = 0; r < SPT; ++r) {
@@ -253,25 +259,34 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
           zw[e] = bload2(zr, o0 < sreal ? o0 : kOob) | (bload2(zr, o1 < sreal ? o1 : kOob) << 16);
         }
       }
+      // entry le of the range is (row, group) = (le / G, le % G): the first
+      // entry's by one division, the rest by stepping (entries below 0 are
+      // skipped and keep row 0)
+      const int lb = pc * 8 - e0;
+      int row = lb > 0 ? (int)p.gdiv.div((uint32_t)lb) : 0;
+      int col = lb - row * p.G;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const int le = pc * 8 + e - e0;
+        const int le = lb + e;
         if (le >= 0 && le < cnt)
-          lds_sz[d0 + le] = ((sw[e >> 1] >> (16 * (e & 1))) & 0xFFFFu) | ((zw[e >> 1] >> (16 * (e & 1))) << 16);
+          lds_sz[d0 + row * SG + col] =
+              ((sw[e >> 1] >> (16 * (e & 1))) & 0xFFFFu) | ((zw[e >> 1] >> (16 * (e & 1))) << 16);
+        if (++col == p.G) { col = 0; ++row; }
       }
     }
   }
+  if (tid < NRANGE * BNO) lds_sz[tid * SG + p.G] = 0u;
   __syncthreads();
   const uint64_t T1 = __builtin_amdgcn_s_memrealtime();
 
   // scale|zero of K-tile t for each block; K-tiles past the wave's range
   // get (0, 0), so their (zero) activations meet zero weights.  Block j's
   // lane c is table row 16j + c (SwiGLU: up rows from BNO on).
+  const int szrow = c * SG;
   auto read_sz = [&](int t, uint32_t (&dst)[NB]) {
-    const int g = p.gshift >= 31 ? 0 : min((t * 64 + 16 * q) >> p.gshift, p.G - 1);
-    const uint32_t keep = t < kt1 ? 0xFFFFFFFFu : 0u;
+    const int g = t >= kt1 ? p.G : p.gshift >= 31 ? 0 : min((t * 64 + 16 * q) >> p.gshift, p.G - 1);
 #pragma unroll
-    for (int j = 0; j < NB; ++j) dst[j] = lds_sz[(16 * j + c) * p.G + g] & keep;
+    for (int j = 0; j < NB; ++j) dst[j] = lds_sz[szrow + 16 * j * SG + g];
   };
 
   f4 acc[MBK][NB];
@@ -610,6 +625,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 // (80 gate + 80 up) weight columns.  SwiGLU with more than 64 rows is left
 // to the other prefill kernels (its 128-row partials would not fit the
 // activation space).
+int g16_sg(int G) { return G + 1 + (G & 1); }
+
 struct G16Shape {
   int mbk, nb;
   bool swi;
@@ -635,9 +652,11 @@ bool shape_ok(const LinearArgs& a) {
   // 32-bit buffer offsets
   if ((int64_t)a.M * a.lda * 2 >= (1ll << 31) || (int64_t)a.N * a.ldw >= (1ll << 31)) return false;
   if ((int64_t)a.N * a.G * 2 >= (1ll << 31)) return false;
-  // scale|zero table: all weight rows of a tile, at most 4 pieces per thread and range
+  // scale|zero table: all weight rows of a tile (rows of g16_sg(G) entries), at
+  // most 4 pieces per thread and range
   const int64_t range = (int64_t)(sh.swi ? 8 : 16) * sh.nb * a.G;
-  if (range * (sh.swi ? 2 : 1) > G16_SZT || range + 8 > 8 * 256 * 4) return false;
+  const int64_t rows = (int64_t)(sh.swi ? 8 : 16) * sh.nb * (sh.swi ? 2 : 1);
+  if (rows * g16_sg(a.G) > G16_SZT || range + 8 > 8 * 256 * 4) return false;
   return a.zeros != nullptr;
 }
 
@@ -673,6 +692,8 @@ hipError_t gemm16_launch(const LinearArgs& a, hipStream_t s, uint64_t* trace) {
   k.gshift = a.g >= a.K ? 31 : __builtin_ctz((unsigned)a.g);
   k.nbm = (a.M + 16 * sh.mbk - 1) / (16 * sh.mbk);
   k.KT = a.K / G16_KT;
+  k.SG = g16_sg(a.G);
+  k.gdiv = Div32::make((uint32_t)a.G);
   const int nwg = gemm16_workgroups(a);
   k.xcd = nwg % 8 == 0;
   k.vec_store = (a.ldc % 8 == 0) && (((uintptr_t)a.C & 15) == 0);
