@@ -13,14 +13,56 @@
 namespace mq {
 namespace {
 
+// Cross-lane exchanges without the LDS unit: within 16-lane rows by DPP
+// (quad_perm, row_mirror 0x140, row_half_mirror 0x141), across rows by the
+// permlane swaps.  xor_lane(v, b) is v of lane (lane ^ b), b a power of two
+// known after unrolling.
+__device__ __forceinline__ int dpp_(int x, int ctrl) {
+  switch (ctrl) {   // the control must be a constant of the instruction
+    case 0xB1: return __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false);   // quad_perm [1,0,3,2]
+    case 0x4E: return __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false);   // quad_perm [2,3,0,1]
+    case 0x1B: return __builtin_amdgcn_update_dpp(0, x, 0x1B, 0xF, 0xF, false);   // quad_perm [3,2,1,0]
+    case 0x140: return __builtin_amdgcn_update_dpp(0, x, 0x140, 0xF, 0xF, false); // row_mirror: ^15
+    default: return __builtin_amdgcn_update_dpp(0, x, 0x141, 0xF, 0xF, false);    // row_half_mirror: ^7
+  }
+}
+// v of lane n of the lane's 16-lane row (DPP row_newbcast)
+__device__ __forceinline__ float row_bcast(float v, int n) {
+  const int x = __float_as_int(v);
+#define RB(k) \
+  case k: return __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0x150 + k, 0xF, 0xF, false));
+  switch (n) {
+    RB(0) RB(1) RB(2) RB(3) RB(4) RB(5) RB(6) RB(7) RB(8) RB(9) RB(10) RB(11) RB(12) RB(13) RB(14)
+    default: return __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0x15F, 0xF, 0xF, false));
+  }
+#undef RB
+}
+__device__ __forceinline__ float xor_lane(float v, int b) {
+  const int x = __float_as_int(v);
+  const bool hi = (threadIdx.x & b) != 0;
+  switch (b) {
+    case 1: return __int_as_float(dpp_(x, 0xB1));
+    case 2: return __int_as_float(dpp_(x, 0x4E));
+    case 4: return __int_as_float(dpp_(dpp_(x, 0x141), 0x1B));    // (^7) then (^3)
+    case 8: return __int_as_float(dpp_(dpp_(x, 0x140), 0x141));   // (^15) then (^7)
+    case 16: {
+      const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);   // rows (0,0,2,2), (1,1,3,3)
+      return __int_as_float(hi ? (int)r[0] : (int)r[1]);
+    }
+    default: {
+      const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);   // halves (0,0), (1,1)
+      return __int_as_float(hi ? (int)r[0] : (int)r[1]);
+    }
+  }
+}
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  for (int o = 32; o > 0; o >>= 1) v += xor_lane(v, o);
   return v;
 }
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, xor_lane(v, o));
   return v;
 }
 // block-wide reduction through LDS (blockDim a multiple of 64, <= 1024)
@@ -389,11 +431,11 @@ __global__ __launch_bounds__(768) void attn_head_d_kernel(const _Float16* qkv, c
       for (int k = 0; k < S / 2; ++k) {
         const float keep = up ? d[k + S / 2] : d[k];
         const float send = up ? d[k] : d[k + S / 2];
-        d[k] = keep + __shfl_xor(send, b);
+        d[k] = keep + xor_lane(send, b);
       }
     }
 #pragma unroll
-    for (int b = DUP / 2; b >= 1; b >>= 1) d[0] += __shfl_xor(d[0], b);
+    for (int b = DUP / 2; b >= 1; b >>= 1) d[0] += xor_lane(d[0], b);
     const int t = t0 + RPI * (q / DUP) + rg;   // the position whose full score this lane holds
     const float sc = t < n ? d[0] * scale : -INFINITY;
     const float m = wave_max(sc);
@@ -402,7 +444,11 @@ __global__ __launch_bounds__(768) void attn_head_d_kernel(const _Float16* qkv, c
     float o[8] = {};
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
-      const float pi = __shfl(p, rg * LPR + i * DUP);   // row i of this row group
+      float pi;   // p of row i of this row group: lane i * DUP of it
+      if constexpr (LPR == 16)
+        pi = row_bcast(p, i * DUP);
+      else
+        pi = __shfl(p, rg * LPR + i * DUP);
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[e] += pi * (float)vv[i][e];
     }
@@ -413,7 +459,7 @@ __global__ __launch_bounds__(768) void attn_head_d_kernel(const _Float16* qkv, c
 #pragma unroll
     for (int b = LPR; b < 64; b <<= 1)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] += __shfl_xor(o[e], b);
+      for (int e = 0; e < 8; ++e) o[e] += xor_lane(o[e], b);
     const float mn = fmaxf(m_run, m);
     const float a = m_run == -INFINITY ? 0.f : expf(m_run - mn), bsc = expf(m - mn);
     l_run = l_run * a + l * bsc;
