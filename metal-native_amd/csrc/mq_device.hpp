@@ -42,6 +42,49 @@ template <> struct FmtTraits<FMT_INT4> { static constexpr int KPL = 32; };
 template <> struct FmtTraits<FMT_INT8> { static constexpr int KPL = 16; };
 template <> struct FmtTraits<FMT_F16>  { static constexpr int KPL = 8; };
 
+// Cross-lane exchanges without the LDS unit: within 16-lane rows by DPP
+// (quad_perm, row_mirror 0x140, row_half_mirror 0x141), across rows by the
+// permlane swaps.  xor_lane(v, b) is v of lane (lane ^ b), b a power of two
+// known after unrolling.
+__device__ __forceinline__ int dpp_(int x, int ctrl) {
+  switch (ctrl) {   // the control must be a constant of the instruction
+    case 0xB1: return __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false);   // quad_perm [1,0,3,2]
+    case 0x4E: return __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false);   // quad_perm [2,3,0,1]
+    case 0x1B: return __builtin_amdgcn_update_dpp(0, x, 0x1B, 0xF, 0xF, false);   // quad_perm [3,2,1,0]
+    case 0x140: return __builtin_amdgcn_update_dpp(0, x, 0x140, 0xF, 0xF, false); // row_mirror: ^15
+    default: return __builtin_amdgcn_update_dpp(0, x, 0x141, 0xF, 0xF, false);    // row_half_mirror: ^7
+  }
+}
+// v of lane n of the lane's 16-lane row (DPP row_newbcast)
+__device__ __forceinline__ float row_bcast(float v, int n) {
+  const int x = __float_as_int(v);
+#define RB(k) \
+  case k: return __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0x150 + k, 0xF, 0xF, false));
+  switch (n) {
+    RB(0) RB(1) RB(2) RB(3) RB(4) RB(5) RB(6) RB(7) RB(8) RB(9) RB(10) RB(11) RB(12) RB(13) RB(14)
+    default: return __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0x15F, 0xF, 0xF, false));
+  }
+#undef RB
+}
+__device__ __forceinline__ float xor_lane(float v, int b) {
+  const int x = __float_as_int(v);
+  const bool hi = (threadIdx.x & b) != 0;
+  switch (b) {
+    case 1: return __int_as_float(dpp_(x, 0xB1));
+    case 2: return __int_as_float(dpp_(x, 0x4E));
+    case 4: return __int_as_float(dpp_(dpp_(x, 0x141), 0x1B));    // (^7) then (^3)
+    case 8: return __int_as_float(dpp_(dpp_(x, 0x140), 0x141));   // (^15) then (^7)
+    case 16: {
+      const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);   // rows (0,0,2,2), (1,1,3,3)
+      return __int_as_float(hi ? (int)r[0] : (int)r[1]);
+    }
+    default: {
+      const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);   // halves (0,0), (1,1)
+      return __int_as_float(hi ? (int)r[0] : (int)r[1]);
+    }
+  }
+}
+
 __device__ __forceinline__ h2 as_h2(uint32_t v) { return __builtin_bit_cast(h2, v); }
 __device__ __forceinline__ uint32_t as_u32(h2 v) { return __builtin_bit_cast(uint32_t, v); }
 

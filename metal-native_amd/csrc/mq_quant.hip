@@ -29,12 +29,12 @@ namespace {
 
 __device__ __forceinline__ float wave_min(float v) {
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fminf(v, __shfl_xor(v, o));
+  for (int o = 32; o > 0; o >>= 1) v = fminf(v, xor_lane(v, o));
   return v;
 }
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, xor_lane(v, o));
   return v;
 }
 
@@ -171,7 +171,7 @@ __global__ __launch_bounds__(256) void quantize_vec_kernel(QuantizeArgs p, int l
   }
   uint32_t pr = __builtin_bit_cast(uint32_t, m);
   for (int o = 1; o < L; o <<= 1)
-    pr = __builtin_bit_cast(uint32_t, __builtin_elementwise_min(as_h2(pr), as_h2((uint32_t)__shfl_xor((int)pr, o))));
+    pr = __builtin_bit_cast(uint32_t, __builtin_elementwise_min(as_h2(pr), as_h2((uint32_t)__float_as_int(xor_lane(__int_as_float((int)pr), o)))));
   const float lo = (float)as_h2(pr).x, hi = -(float)as_h2(pr).y;
   float sf, zp = 0.f;
   _Float16 s16, z16 = (_Float16)0.f;

@@ -322,7 +322,7 @@ __global__ __launch_bounds__(64 * NW) void rows_kernel(RowsKArgs p) {
         }
       }
 #pragma unroll
-      for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+      for (int o = 32; o > 0; o >>= 1) ss += xor_lane(ss, o);
       float* red = (float*)(smem + p.off_scr);   // per-wave scratch, free until the first tile fold
       if (lane == 0) red[w * 256] = ss;
       asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");

@@ -121,7 +121,7 @@ __global__ __launch_bounds__(256) void vecmat32_nk_kernel(const float* A, int64_
     for (int m = 0; m < M; ++m) {
       float v = acc[r][m];
 #pragma unroll
-      for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+      for (int o = 32; o > 0; o >>= 1) v += xor_lane(v, o);
       if (lane == 0 && n0 + r < N) C[(int64_t)m * ldc + n0 + r] = v;
     }
 }
@@ -216,10 +216,10 @@ __global__ __launch_bounds__(64 * kWavesKV) void vecmat32_kn4_kernel(const float
   for (int m = 0; m < M; ++m) {
 #pragma unroll
     for (int o = 16; o < 64; o <<= 1) {
-      acc[m].x += __shfl_xor(acc[m].x, o);
-      acc[m].y += __shfl_xor(acc[m].y, o);
-      acc[m].z += __shfl_xor(acc[m].z, o);
-      acc[m].w += __shfl_xor(acc[m].w, o);
+      acc[m].x += xor_lane(acc[m].x, o);
+      acc[m].y += xor_lane(acc[m].y, o);
+      acc[m].z += xor_lane(acc[m].z, o);
+      acc[m].w += xor_lane(acc[m].w, o);
     }
     if (lane < 16) red[w][m][cg] = acc[m];
   }
