@@ -141,6 +141,19 @@ bool gemm16_auto(const mq::LinearArgs& a) {
   return 4 * (int64_t)mq::gemm16_workgroups(a) >= 3 * (int64_t)num_cus_current() && 4 * (int64_t)a.M >= 3 * mpad;
 }
 
+// Short weight rows over many of them, M <= 4: the split-K GEMV, whose
+// start-up is shorter than the row-block kernel's staging of all of K.
+// Measured on 108 shapes (M = 1, 2, 4; K = 512..3584; N = 896, 4864, 14336;
+// int4 g64 and int8 per-channel): it is faster for K <= 896 from N = 4864
+// (config 1, K = 896, N = 4864: 4.0 vs 5.2 us) and for int4 at K = 1536
+// with M <= 2 (4.6 vs 5.6 us at N = 4864), slower at N = 896 and from K = 2048.
+bool short_rows(const mq::LinearArgs& a) {
+  if (a.prenorm || a.fmt == mq::FMT_F16) return false;
+  const int64_t nrows = a.epi == mq::EPI_SWIGLU ? a.F : a.N;
+  if (nrows < 2048) return false;
+  return a.K <= 1024 || (a.fmt == mq::FMT_INT4 && a.M <= 2 && a.K <= 1536);
+}
+
 int choose_path(const mq::LinearArgs& a, bool noalloc) {
   int forced = g_force_path.load();
   if (forced == PATH_ROWS && rows_ok(a)) return PATH_ROWS;
@@ -152,6 +165,7 @@ int choose_path(const mq::LinearArgs& a, bool noalloc) {
   // where the activations fit in LDS whole (its K parts measured slower than
   // the split-K GEMV at config 2, M = 8: 20.3 vs 18.2 us; whole, it is
   // faster: config 4 at M = 8, 29.5 vs 40.3 us, at M = 16, 31.8 vs 45.4 us)
+  if (a.M <= 4 && short_rows(a) && decode_ok(a)) return PATH_DECODE;
   if (a.M <= 4 && rows_ok(a)) return PATH_ROWS;
   if (a.M <= 16) {
     const mq::RowsPlan pl = mq::rows_plan(a, num_cus_current());
@@ -214,6 +228,18 @@ int run_linear(const mq::LinearArgs& a, hipStream_t s, bool noalloc = false) {
       }
     } else {
       e = workspace_for(s, pl.ws_bytes, &ws);
+      if (e == hipErrorStreamCaptureUnsupported && a.M <= 4 && rows_ok(a)) {
+        // under capture with a workspace too small for this shape: the
+        // row-block kernel in one part (no workspace) rather than an error
+        const mq::RowsPlan rp = mq::rows_plan(a, num_cus_current(), false);
+        if (rp.ok) {
+          path = PATH_ROWS;
+          e = mq::rows_launch(a, rp, nullptr, s);
+          if (e != hipSuccess) return hip_fail(e, "dequant_matmul: kernel launch failed");
+          g_last_path = path;
+          return MQ_SUCCESS;
+        }
+      }
       if (e == hipErrorStreamCaptureUnsupported)
         return fail(MQ_INVALID_ARGUMENT, "dequant_matmul: the split-K workspace of this stream is too small; "
                                          "make one call of this shape on the stream before capturing it");

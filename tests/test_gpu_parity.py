@@ -248,7 +248,10 @@ def test_config2_qwen7b_down(mn, gpu, M):
 
 @pytest.mark.parametrize("M,K,N,want", [(16, 18944, 3584, "gemmw_split"), (9, 18944, 3584, "gemmw_split"),
                                          (8, 18944, 3584, "rstream"), (16, 4096, 4096, "decode"),
-                                         (32, 18944, 3584, "gemmw_split")])
+                                         (32, 18944, 3584, "gemmw_split"),
+                                         # short rows at M <= 4: the split-K GEMV from N = 2048
+                                         (1, 896, 4864, "decode"), (2, 1536, 4864, "decode"),
+                                         (4, 1536, 4864, "rows"), (1, 896, 1024, "rows"), (1, 2048, 4864, "rows")])
 def test_mid_band_routing(mn, gpu, M, K, N, want):
     """Between the decode GEMVs and the prefill GEMM: at M = 9..16 with K >=
     8192 the prefill GEMM with K split over workgroups is taken where it
@@ -506,6 +509,32 @@ def test_hip_graph_replay(mn, gpu):
         np.testing.assert_array_equal(out.cpu().numpy().view(np.uint16), eager.view(np.uint16),
                                       err_msg=f"replay {rep}")
         _ = host(mn.dequant_matmul(xa[:1].contiguous(), wa, sa, za, 128, "int4"))  # eager work between
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 896, 4864), (2, 1536, 4864)])
+def test_short_rows_capture_on_a_fresh_stream(mn, gpu, M, K, N):
+    """A short-row decode shape (the split-K GEMV by default) captured first
+    on a stream that has no workspace yet: the capture succeeds (the GEMV
+    without a workspace, or the row-block kernel in one part where the GEMV
+    would need one) and every replay matches the oracle."""
+    say(f"short rows under capture M={M} K={K} N={N}")
+    g = 128
+    x, wp, s, z = O.make_int4_problem(M, K, N, g, seed=K + M)
+    ref = O.matmul_f32acc(x, O.dequant_int4(wp, s, z, K, g))
+    xa, wa, sa, za = (dev(v, gpu) for v in (x, wp, s, z))
+    check_close(host(mn.dequant_matmul(xa, wa, sa, za, g, "int4")), ref, "short rows eager")
+    stream = torch.cuda.Stream()   # no call on it yet: no workspace
+    stream.wait_stream(torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        out = mn.dequant_matmul(xa, wa, sa, za, g, "int4")
+    assert mn.last_path() in ("decode", "rows"), mn.last_path()
+    for rep in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        check_close(host(out), ref, f"short rows replay {rep}")
+        _ = host(mn.dequant_matmul(xa, wa, sa, za, g, "int4"))   # eager work between
 
 
 def test_graph_survives_workspace_growth(mn, gpu):
