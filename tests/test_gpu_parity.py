@@ -269,12 +269,16 @@ def test_mid_band_routing(mn, gpu, M, K, N, want):
         check_close(y2, ref, "mid band decode")
 
 
-def test_config1_qwen05b_gate(mn, gpu):
-    say("config1")
+@pytest.mark.parametrize("path", [None, "rows", "decode"])
+def test_config1_qwen05b_gate(mn, gpu, path):
+    """Config 1 at full size: the automatic route (the split-K GEMV for these
+    short rows) and the row-block kernel forced."""
+    say(f"config1 {path}")
     x, wp, s, z = O.make_int4_problem(1, 896, 4864, 64, seed=0)
     ref = O.matmul_f32acc(x, O.dequant_int4(wp, s, z, 896, 64))
-    y, _ = run_dm(mn, gpu, x, wp, s, z, 64, "int4")
-    check_close(y, ref, "config1")
+    y, taken = run_dm(mn, gpu, x, wp, s, z, 64, "int4", path)
+    assert taken == (path or "decode"), taken
+    check_close(y, ref, f"config1 [{taken}]")
 
 
 @pytest.mark.parametrize("g", [128, 64, 32])
