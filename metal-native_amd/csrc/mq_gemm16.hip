@@ -115,23 +115,25 @@ __host__ __device__ constexpr int g16_rank(int ww, int i, int j) {
 
 template <int FMT, int MBK, int NB, bool SWI>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm16_kernel(G16Args p) {
-  constexpr int WPF = FMT == FMT_INT4 ? 4 : 2;  // weight ring depth in K-tiles
+  // weight ring depth in K-tiles: 2 (with a 4-deep ring the int4 kernel
+  // measured 1.5-3 % slower at config 3, g = 128 / 64 / 32)
+  constexpr int WPF = 2;
   constexpr int NBU = SWI ? NB / 2 : NB;        // output blocks per row block
   constexpr int BNO = 16 * NBU;                 // output columns per tile
   constexpr int BM = 16 * MBK;                  // rows per tile
   constexpr int SLOTU = BM * 8;                 // 16-byte pieces per activation slot (BM rows x 64 k)
   constexpr int NS = G16_AU / SLOTU;            // 16-byte slots of the wave's activation space
   // activation ring depth: 2 slots (one K-tile of lead beyond the current);
-  // with a 2-deep weight ring too the K-tile loop is unrolled by 2, so a
-  // wave's last K-tiles fill the unroll (int8: 14 K-tiles per wave at config
-  // 4, which a 4-tile unroll would round up to 16)
-  constexpr int NSA = WPF == 2 ? 2 : NS;
-  constexpr int UNR = WPF > NSA ? WPF : NSA;     // K-tiles per loop iteration
+  // with the 2-deep weight ring the K-tile loop is unrolled by 2 (static ring
+  // indices), so a wave's last K-tiles fill the unroll (int8: 14 K-tiles per
+  // wave at config 4, which a 4-tile unroll would round up to 16)
+  constexpr int NSA = 2;
+  constexpr int UNR = 2;                        // K-tiles per loop iteration
   constexpr int NDMA = 2 * MBK;                 // DMA instructions per K-tile (8 rows each)
   constexpr int WB = FMT == FMT_INT4 ? 8 : 16;  // weight bytes per lane per K-tile
   constexpr int NRANGE = SWI ? 2 : 1;           // weight row ranges (gate, up)
   static_assert(NS == 2 || NS == 4, "the activation space is 2 or 4 slots");
-  static_assert(UNR == 2 || UNR == 4, "the K-tile loop is unrolled by 2 or 4");
+  static_assert(NSA <= NS && WPF == UNR && NSA == UNR, "the rings rotate with the 2-tile unroll");
   static_assert(!SWI || NB % 2 == 0, "SwiGLU pairs gate and up blocks");
   static_assert(MBK * NB - (MBK * NB) / 4 <= 32, "a wave's partials fit in its activation space");
   typedef typename std::conditional<FMT == FMT_INT4, u2v, u4>::type WReg;
@@ -432,12 +434,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     u4* const nxt = slot(std::integral_constant<int, (R + 1) % NSA>{});
     if (R == 0 && t == kt0) {   // the first K-tile: the rest of the prologue
       dma_tile(kt0 + 1, slot(std::integral_constant<int, 1>{}));
-      if constexpr (NSA > 2) {
-        dma_tile(kt0 + 2, slot(std::integral_constant<int, 2 % NSA>{}));
-        dma_tile(kt0 + 3, slot(std::integral_constant<int, 3 % NSA>{}));
-      }
-#pragma unroll
-      for (int d = 2; d < WPF; ++d) load_w(kt0 + d, wring[d]);
     }
     read_sz(t + 1, sz2);
     // k-step 0 of tile t: reads all of k-step 1's fragments first; once
@@ -455,17 +451,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
     for (int j = 0; j < NB; ++j) sz[j] = sz2[j];
   };
-  // UNR K-tiles per iteration (static ring indices: no register copies of
+  // two K-tiles per iteration (static ring indices: no register copies of
   // loads in flight); a K-tile past the wave's range reads zeros and has
   // zero scales
   int t = kt0;
   do {
     tile(std::integral_constant<int, 0>{}, t);
     tile(std::integral_constant<int, 1>{}, t + 1);
-    if constexpr (UNR == 4) {
-      tile(std::integral_constant<int, 2 % UNR>{}, t + 2);
-      tile(std::integral_constant<int, 3 % UNR>{}, t + 3);
-    }
     t += UNR;
   } while (t < kt1);
   const uint64_t T2 = __builtin_amdgcn_s_memrealtime();
