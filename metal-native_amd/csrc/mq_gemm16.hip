@@ -13,16 +13,16 @@
 //
 // Structure:
 //  * Workgroup = 4 waves (one per SIMD) on one output tile of 16*MBK rows by
-//    16*NB weight columns.  Wave w takes the w-th quarter of the 64-k
-//    K-tiles, so every weight is loaded and dequantized once per workgroup
-//    and every activation moved once.
+//    16*NB weight columns.  Wave w takes every fourth 64-k K-tile from the
+//    w-th, so every weight is loaded and dequantized once per workgroup and
+//    every activation moved once.
 //  * Activations: direct-to-LDS 16-byte loads (buffer_load ... lds), fully
 //    coalesced, in a ring of 2 slots per wave (16 KiB for 128-row tiles,
 //    8 KiB for 64-row tiles; 32 KiB per wave in all, the rest used by the
 //    partial exchange), XOR-swizzled so that the fragment reads (one row per
 //    lane) are bank-conflict free.  A K-tile's second k-step fragments are
-//    read first, so its slot is refilled (K-tile t+2) while its first k-step
-//    computes.
+//    read first, so its slot is refilled (the wave's K-tile after next)
+//    while its first k-step computes.
 //  * Weights: lane (c, q) of block j loads the 16 k at 64t + 16q of its
 //    column (8 bytes int4, 16 bytes int8): the first half is its B operand
 //    of the tile's first k-step, the second half of the second (k-step s
@@ -157,7 +157,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   const rsrc_t sr = make_rsrc(p.scales, p.s_bytes);
   const rsrc_t zr = make_rsrc(p.zeros, p.s_bytes);
   const rsrc_t nullr = make_rsrc(p.A, 0);   // every load through it reads zeros
-  const int kt0 = (w * p.KT) / 4, kt1 = ((w + 1) * p.KT) / 4;
+  // wave w takes K-tiles w, w + 4, w + 8, ...: the four waves read
+  // neighbouring 64-k pieces of the same activation and weight rows at once
+  // (contiguous quarters of K measured 1-3.5 % slower at configs 3 and 4)
+  constexpr int TS = 4;   // K-tile stride of a wave
+  const int kt0 = w, kt1 = p.KT;
   const int ncols = min(BNO, p.F - n0);     // real output columns of the tile
 
   // ---- scale | zero table, first: per weight row range (the tile's
@@ -237,7 +241,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   // would hold back the first data: every CU starts at once)
   dma_tile(kt0, slot(std::integral_constant<int, 0>{}));
   load_w(kt0, wring[0]);
-  load_w(kt0 + 1, wring[1]);
+  load_w(kt0 + TS, wring[1]);
   // scale | zero table writes (s | z << 16 per entry; range rg from row
   // rg * BNO), then the zero column
   const int SG = p.SG;
@@ -425,28 +429,29 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     }
   }
 
-  // K-tile t (t - kt0 = R mod UNR): activations in slot R % NSA, weights in
-  // ring slot R % WPF; the next K-tile's activations are in slot (R+1) % NSA.
+  // the wave's K-tile t ((t - kt0) / TS = R mod UNR): activations in slot
+  // R % NSA, weights in ring slot R % WPF; the wave's next K-tile (t + TS)
+  // has its activations in slot (R+1) % NSA.
   auto tile = [&](auto rc, int t) {
     constexpr int R = decltype(rc)::value;
     constexpr int RW = R % WPF, RW1 = (R + 1) % WPF;
     u4* const cur = slot(std::integral_constant<int, R % NSA>{});
     u4* const nxt = slot(std::integral_constant<int, (R + 1) % NSA>{});
     if (R == 0 && t == kt0) {   // the first K-tile: the rest of the prologue
-      dma_tile(kt0 + 1, slot(std::integral_constant<int, 1>{}));
+      dma_tile(kt0 + TS, slot(std::integral_constant<int, 1>{}));
     }
-    read_sz(t + 1, sz2);
+    read_sz(t + TS, sz2);
     // k-step 0 of tile t: reads all of k-step 1's fragments first; once
-    // they are in registers the slot is refilled (K-tile t+NSA), spread over
+    // they are in registers the slot is refilled (K-tile t + NSA TS), spread over
     // the rest of the k-step; then the weight slot is refilled
     step(std::true_type{}, afA, bqA, cur, 1, afB, wring[RW], sz, 1, bqB, [&](int j) {
       if (j == 0) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
       for (int i = 0; i < NDMA; ++i)
-        if ((i * NB) / NDMA == j) dma_one(t + NSA, cur, i);
+        if ((i * NB) / NDMA == j) dma_one(t + NSA * TS, cur, i);
     });
-    load_w(t + WPF, wring[RW]);
-    // k-step 1 of tile t; prepares tile t+1's k-step 0 from slot `nxt`
+    load_w(t + WPF * TS, wring[RW]);
+    // k-step 1 of tile t; prepares tile t + TS's k-step 0 from slot `nxt`
     step(std::false_type{}, afB, bqB, nxt, 0, afA, wring[RW1], sz2, 0, bqA, [&](int) {});
 #pragma unroll
     for (int j = 0; j < NB; ++j) sz[j] = sz2[j];
@@ -457,8 +462,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   int t = kt0;
   do {
     tile(std::integral_constant<int, 0>{}, t);
-    tile(std::integral_constant<int, 1>{}, t + 1);
-    t += UNR;
+    tile(std::integral_constant<int, 1>{}, t + TS);
+    t += UNR * TS;
   } while (t < kt1);
   const uint64_t T2 = __builtin_amdgcn_s_memrealtime();
 
