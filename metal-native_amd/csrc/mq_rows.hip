@@ -48,7 +48,12 @@
 namespace mq {
 namespace {
 
-constexpr int kD = 4;        // ring depth (units in flight per wave)
+// ring depth (units in flight per wave): 3 for int4, whose loop is bound by
+// the dequant issue (config 2 M=1: 11.6-11.8 vs 11.9-12.4 us with 4, M=4
+// 15.1-15.3 vs 15.5-15.7), 4 for int8 and fp16, which wait on the stream
+// (config 4 M=1: 25.8-26.3 vs 26.1-26.6 us with 3; 2 is slower for both)
+template <int FMT>
+constexpr int ring_depth() { return FMT == FMT_INT4 ? 3 : 4; }
 // wavefronts per workgroup: 12, or 8 when the workgroup streams at most
 // kSmallBytes of weights (measured at M = 1: 8 waves 4-8 % faster at 2-8 MB
 // in total, 3-4 % slower at 34 MB and more)
@@ -272,6 +277,7 @@ __global__ __launch_bounds__(64 * NW) void rows_kernel(RowsKArgs p) {
     }
   };
 
+  constexpr int kD = ring_depth<FMT>();
   u4 raw[kD];
   {
     u4 xv[kXB];
