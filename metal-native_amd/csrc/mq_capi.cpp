@@ -171,12 +171,15 @@ int choose_path(const mq::LinearArgs& a, bool noalloc) {
     const mq::RowsPlan pl = mq::rows_plan(a, num_cus_current());
     if (pl.ok && pl.KP == 1) return PATH_ROWS;
   }
-  // M = 5..8 whose activations do not fit in LDS whole: the register-streamed
-  // GEMV (no K parts, no workspace; config 2 at M = 5 / 8: 15.0 / 16.1 us
-  // against 17.0 / 18.5 us for the row-block kernel's K parts and 17.6 us
-  // for the split-K GEMV at M = 8)
-  if (a.M >= 5 && a.M <= 8 && mq::rstream_plan(a, num_cus_current()).ok) return PATH_RSTREAM;
-  // M = 9..16 with long rows: the prefill GEMM with K split over
+  // M = 5..16 whose activations do not fit in LDS whole: the register-streamed
+  // GEMV where its plan takes the shape (no K parts, no workspace; config 2 at
+  // M = 5 / 8: 15.0 / 16.1 us against 17.0 / 18.5 us for the row-block
+  // kernel's K parts and 17.6 us for the split-K GEMV at M = 8; at M = 9..16
+  // 6-45 % faster than both the K-split prefill GEMM and the split-K GEMV
+  // on 13 shapes, e.g. config 2 at M = 9 / 16: 19.0-19.7 / 21.6 us against
+  // 25.0 / 25.4 us, K = 4096, N = 4096, M = 16: 8.3 against 12.0 us)
+  if (a.M >= 5 && a.M <= 16 && mq::rstream_plan(a, num_cus_current()).ok) return PATH_RSTREAM;
+  // M = 9..16 with long rows the register-streamed plan declines: the prefill GEMM with K split over
   // workgroups beats the split-K GEMV (measured at K >= 8192 on 6 shapes at
   // M = 9, 12, 13-16: faster on all but K = 8192, N = 4096 (2-10 % slower
   // at M = 9-16), by up to 45 %, e.g. K = 18944, N = 3584, M = 16: 26.3 vs

@@ -1,6 +1,6 @@
 // Register-streamed row-block decode GEMV for skinny activations whose
 // activation rows do not fit in LDS whole (int4 weights, 3 <= M <= 16, long
-// K; the Qwen2.5-7B down-proj at M = 5..8 is its main case).
+// K; the Qwen2.5-7B down-proj at M = 5..16 is its main case).
 //
 // Replaces, like mq_rows.hip and mq_gemv.hip, the reference's M<=8 routes
 // (shaders/matmul_dequant_kernel.metal:229-345 and :485-576, dispatched at
@@ -335,6 +335,7 @@ hipError_t rs_launch4(const RsArgs& k, int nwg, hipStream_t s) {
 template <int FMT, int EPI, int RPW>
 hipError_t rs_launch3(const RsArgs& k, const RsPlan& pl, hipStream_t s) {
   switch (pl.twm) {
+    case 1: return rs_launch4<FMT, EPI, RPW, 1>(k, pl.nwg, s);
     case 2: return rs_launch4<FMT, EPI, RPW, 2>(k, pl.nwg, s);
     case 4:   // (16-row tiles: at most 2 per workgroup, their partials fill a wave's first slot)
       if constexpr (RPW < 16) return rs_launch4<FMT, EPI, RPW, 4>(k, pl.nwg, s);
@@ -409,7 +410,9 @@ RsPlan rstream_plan(const LinearArgs& a, int num_cus) {
   if ((int64_t)(swi ? a.F + R : R) * a.ldw >= lim) return p;
   if ((int64_t)KS * kstep * (a.fmt == FMT_INT4 ? 1 : 2) / 2 >= lim) return p;
   if ((int64_t)TW * KS * kRsNW >= ((int64_t)1 << 31)) return p;
-  const int twm = TW <= 2 ? 2 : 4;
+  // tiles the per-wave arrays and scale table are sized for (one tile:
+  // the table holds twice the groups, e.g. 14 x 16 rows at K = 18944, M = 16)
+  const int twm = TW == 1 ? 1 : TW <= 2 ? 2 : 4;
   if (best == 16 && twm > 2) return p;
   // every wave's scale table (its tile rows x the groups of its K range)
   const int gs = rs_gshift(a);

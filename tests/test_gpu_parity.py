@@ -246,16 +246,20 @@ def test_config2_qwen7b_down(mn, gpu, M):
         check_close(y, ref, f"config2 M={M} [{path}, {mn.last_path()}]")
 
 
-@pytest.mark.parametrize("M,K,N,want", [(16, 18944, 3584, "gemmw_split"), (9, 18944, 3584, "gemmw_split"),
-                                         (8, 18944, 3584, "rstream"), (16, 4096, 4096, "decode"),
+@pytest.mark.parametrize("M,K,N,want", [(16, 18944, 3584, "rstream"), (9, 18944, 3584, "rstream"),
+                                         (8, 18944, 3584, "rstream"), (16, 4096, 4096, "rstream"),
+                                         (12, 8192, 8192, "rstream"),   # two 16-row tiles per workgroup
+                                         (16, 18944, 7168, "decode"),   # scale table too large for rstream
+                                         (13, 14336, 4096, "rstream"),
                                          (32, 18944, 3584, "gemmw_split"),
                                          # short rows at M <= 4: the split-K GEMV from N = 2048
                                          (1, 896, 4864, "decode"), (2, 1536, 4864, "decode"),
                                          (4, 1536, 4864, "rows"), (1, 896, 1024, "rows"), (1, 2048, 4864, "rows")])
 def test_mid_band_routing(mn, gpu, M, K, N, want):
-    """Between the decode GEMVs and the prefill GEMM: at M = 9..16 with K >=
-    8192 the prefill GEMM with K split over workgroups is taken where it
-    splits; the result matches the oracle on every path."""
+    """Between the decode GEMVs and the prefill GEMM: at M = 5..16 the
+    register-streamed GEMV where its plan takes the shape, else at K >= 8192
+    the prefill GEMM with K split over workgroups where it splits; the result
+    matches the oracle on every path."""
     say(f"mid band M={M} K={K} N={N}")
     g = 128
     x, wp, s, z = O.make_int4_problem(M, K, N, g, seed=M)
@@ -1036,6 +1040,11 @@ def test_one_hot_selects_dequantized_weights(mn, gpu, qt, path, impl, M):
     (4, 2048, 512, 2048, None),        # per-channel scales
     (6, 1024, 40, 128, "bias_relu"),   # fewer rows than CUs
     (8, 512, 2 * 640, 64, "swiglu"),
+    (16, 18944, 3584, 128, None),      # config 2 at M = 16: one 16-row tile per workgroup
+    (12, 8192, 4096, 128, "bias"),
+    (13, 2944, 500, 128, "bias_silu"),  # ragged, one tile
+    (9, 8192, 8192, 128, "residual"),  # two 16-row tiles per workgroup
+    (16, 1024, 2 * 1024, 64, "swiglu"),
 ])
 def test_rstream(mn, gpu, M, K, N, g, epi):
     """The register-streamed GEMV forced on ragged, grouped and per-channel

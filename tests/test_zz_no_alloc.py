@@ -69,9 +69,9 @@ def test_noalloc_rejects_shapes_beyond_the_scratch(forced_split_k, gpu):
     # K parts (workspace), so the no-allocation entry point runs the split-K GEMV
     (4, 18944, 3584, 128, "decode", {"force_path": 6}),
     (1, 18944, 3584, 128, "rows", {}),
-    # middle band: M <= 16 takes the split-K GEMV (fixed scratch), M > 16 the
-    # prefill GEMM without its K split (no workspace)
-    (16, 18944, 3584, 128, "decode", {"force_path": 6}),
+    # middle band: M = 5..16 takes the register-streamed GEMV (no workspace
+    # either way), M > 16 the prefill GEMM without its K split (no workspace)
+    (16, 18944, 3584, 128, "rstream", {}),
     (32, 18944, 3584, 128, "gemmw", {"gemm_split": 0}),
 ])
 def test_noalloc_automatic_paths(gpu, M, K, N, g, want, ref_opts):
