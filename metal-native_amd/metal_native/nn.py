@@ -8,9 +8,10 @@ vecmat kernel, other shapes on torch.matmul as in ``metal_native.matmul``.
 ``QuantizedLinear`` is the quantized counterpart the reference lacks: int4 /
 int8 weights in the reference's storage format with the bias fused into the
 GEMV/GEMM epilogue (``dequant_matmul(..., epilogue="bias")``).  The library
-picks the kernel by the number of rows: the row-block GEMV for M <= 4 (when
-the activations fit in LDS), the split-K GEMV up to M = 16, the MFMA GEMM
-beyond.  Built from fp16 weights (``from_float``, quantized on the GPU by
+picks the kernel by the number of rows: the row-block GEMV for M <= 4, and
+up to M = 16 where the activations fit in LDS; for int4 at M = 5..16 the
+register-streamed GEMV where its plan takes the shape; the split-K GEMV for
+short rows and what the others decline; the MFMA GEMM beyond M = 16.  Built from fp16 weights (``from_float``, quantized on the GPU by
 ``quantize``) or from a ``QuantizedWeight`` (a loaded or converted
 checkpoint, ``from_quantized``).
 """
